@@ -1,0 +1,150 @@
+/*
+ * matrix_amd.h -- C launch ABI of the MI355X (gfx950) evaluation path.
+ *
+ * This is the boundary between the host graph layer (matrix / Primitive, lazy DFS,
+ * compile / execute) and the device.  It replaces the reference's L2 GPU backends and
+ * its Metal device manager:
+ *   - every call is `extern "C"`, takes plain pointers, sizes and uint32 element strides
+ *     (the reference's size_m, Mods/Utils.h:125), and returns an mx_status;
+ *   - nothing throws across it; mx_last_error() gives the message of the last failure on
+ *     the calling thread;
+ *   - launches are asynchronous on the given stream (NULL = the calling thread's stream,
+ *     see mx_hip_stream_for_thread); nothing allocates device memory except mx_hip_alloc;
+ *   - descriptor arrays (shape / strides) are read on the host during the call and may be
+ *     freed as soon as it returns.
+ *
+ * Element type codes are the reference's dtype codes (matrix.h:35-52).
+ */
+#ifndef MATRIX_AMD_H
+#define MATRIX_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ codes */
+typedef enum {
+    MX_OK = 0,
+    MX_ERR_INVALID_ARG = 1,     /* bad shape / stride / rank / null pointer */
+    MX_ERR_UNSUPPORTED = 2,     /* no kernel for this (op, dtype) -- GPUManager.h:64-71 */
+    MX_ERR_HIP = 3,             /* a HIP runtime call failed */
+    MX_ERR_NOT_INITIALIZED = 4, /* mx_hip_init was not called */
+    MX_ERR_WORKSPACE = 5        /* workspace missing or too small */
+} mx_status;
+
+/* dtype codes, matrix.h:35-52 */
+enum {
+    MX_FLOAT32 = 0, MX_FLOAT16 = 1, MX_UINT8 = 2, MX_INT32 = 3, MX_INT16 = 4,
+    MX_UINT32 = 5, MX_UINT16 = 6, MX_BOOL = 7, MX_INT8 = 8, MX_COMPLEX64 = 9,
+    MX_BFLOAT16 = 10, MX_INT64 = 11, MX_UINT64 = 12
+};
+
+/* broadcast binary ops */
+enum { MX_OP_ADD = 0, MX_OP_SUB = 1, MX_OP_MUL = 2, MX_OP_DIV = 3,
+       MX_OP_MAX = 4, MX_OP_MIN = 5, MX_OP_EQ = 6 };
+
+/* reductions */
+enum { MX_RED_SUM = 0, MX_RED_MAX = 1, MX_RED_MIN = 2, MX_RED_ARGMAX = 3, MX_RED_ARGMIN = 4 };
+
+#define MX_MAX_DIMS 8   /* MAX_TENSOR_DIMS, Mods/Utils.h:127 */
+
+const char* mx_last_error(void);
+const char* mx_version(void);
+
+/* ------------------------------------------------------------------ device runtime
+ * Replaces GlobalGPUManager (Mods/GPUManager.h:26-58, GPUManager.h:1261): device + per-thread
+ * stream instead of MTLDevice + thread-local command buffer / encoder. */
+int mx_hip_init(int device);
+int mx_hip_shutdown(void);
+int mx_hip_device_count(int* count);
+
+/* The matrix buffer's MTLBuffer slot (matrix.h:677-680, matrix.h:458-467) becomes a device
+ * allocation; the host matrix keeps the atomic refcount. */
+int mx_hip_alloc(size_t bytes, void** dptr);
+int mx_hip_free(void* dptr);
+int mx_hip_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int mx_hip_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int mx_hip_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int mx_hip_memset(void* dst, int value, size_t bytes, void* stream);
+
+/* getCommandBuffer / commitCommandBuffer (GPUManager.h:540-594, GPUManager.h:558-562):
+ * one stream per host thread; sync waits and reports any asynchronous kernel error. */
+int mx_hip_stream_for_thread(void** stream);
+int mx_hip_sync(void* stream);
+
+/* Timing (the reference's Timer, Mods/Utils.h:316-335, but on the device clock). */
+int mx_hip_event_create(void** event);
+int mx_hip_event_destroy(void* event);
+int mx_hip_event_record(void* event, void* stream);
+int mx_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ------------------------------------------------------------------ kernels */
+
+/* R[i] = A[i] op B[i] over a collapsed broadcast iteration space.
+ * Replaces add/subtract/multiply/divide_gpu_brodcasted (Matrix.mm:7709-8238), the binary
+ * max/min backends (Matrix.mm:13378-13478, Matrix.mm:14668-14783) and equal_backend
+ * (Matrix.mm:14469-14540).  The arrays are exactly CollapsedDims_3 (Mods/Utils.h:142-148)
+ * from collapse_dims (Mods/Utils.mm:169-202): shape, stridesC (= sR), stridesA, stridesB.
+ * cdims == 0 is the rank-0 case (Matrix.mm:7460-7469).  A, B and R share one dtype. */
+int mx_launch_bcast_binary(int op, int dtype, int cdims, const uint32_t* shape,
+                           const uint32_t* sR, const uint32_t* sA, const uint32_t* sB,
+                           void* R, const void* A, const void* B, void* stream);
+
+/* out[g] = reduce_{i < n_reduce} in[offset(g) + i * reduce_stride] for every output g,
+ * out written contiguously.  Replaces sum(out, axis, keepdims, dev) (Matrix.mm:15099-15208),
+ * max / min (Matrix.mm:14812-15059) and argmax / argmin (Matrix.mm:16182-16458).  The arrays
+ * are exactly CollapsedDims_2 from collapse_dims_reduce (Mods/Utils.mm:321-376): shape,
+ * stridesA (= sOut), stridesB (= sIn); reduce_stride / n_reduce are strides()[axis] and
+ * shape()[axis] (Matrix.mm:15104-15105).  ARGMAX / ARGMIN write int32.  The workspace holds
+ * the second pass's partials; its size comes from mx_reduce_workspace_bytes (0 is valid when
+ * that returns 0). */
+int mx_reduce_workspace_bytes(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduce,
+                              int cdims, const uint32_t* shape, const uint32_t* sOut,
+                              const uint32_t* sIn, size_t* bytes);
+int mx_launch_reduce(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduce,
+                     int cdims, const uint32_t* shape, const uint32_t* sOut, const uint32_t* sIn,
+                     void* out, const void* in, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* C[b, m, n] = sum_k A[b, m, k] * Bt[b, n, k].  Replaces dot_gpu / batched_dot_gpu
+ * (Matrix.mm:7198-7291).  The arrays are exactly CollapsedDims_3 from collapse_dims_matmul
+ * (Mods/Utils.mm:204-252): shapeC = [batch..., M, N], sA / sBt / sC per axis, whose last
+ * entry is the K stride of A and of Bt (the reference requires 1 there; any value is
+ * accepted here) and the N stride of C.  float32 runs on fp32 MFMA, float16 / bfloat16 on
+ * 16-bit MFMA with fp32 accumulation; integer types accumulate in their own type (wrap). */
+int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC,
+                             const uint32_t* sA, const uint32_t* sBt, const uint32_t* sC,
+                             uint32_t K, void* C, const void* A, const void* Bt, void* stream);
+
+/* Channels-last N-D convolution, the argument set of conv_gpu (Matrix.mm:12335-12395) /
+ * conv2d_gpu (Matrix.mm:5521-5559): input [N, S1..Sn, C], kernel [O, K1..Kn, C/groups],
+ * output [N, O1..On, O], each with arbitrary element strides; pad_lo / stride / dil_rhs
+ * (kernel dilation) / dil_lhs (input dilation) have nspatial entries; flip != 0 reads the
+ * kernel back to front.  Operands that are not channel-contiguous are packed into the
+ * workspace first (size from mx_conv_workspace_bytes). */
+int mx_conv_workspace_bytes(int dtype, int nspatial, const uint32_t* in_shape,
+                            const uint32_t* k_shape, const uint32_t* out_shape,
+                            const uint32_t* in_strides, const uint32_t* k_strides,
+                            const uint32_t* out_strides, int groups, size_t* bytes);
+int mx_launch_conv_nd(int dtype, int nspatial, const uint32_t* in_shape,
+                      const uint32_t* k_shape, const uint32_t* out_shape,
+                      const uint32_t* in_strides, const uint32_t* k_strides,
+                      const uint32_t* out_strides, const int* pad_lo, const int* stride,
+                      const int* dil_rhs, const int* dil_lhs, int groups, int flip,
+                      void* out, const void* in, const void* kern,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* dst[sum idx * sDst] = cast(src[sum idx * sSrc]) over a collapsed space.  Replaces
+ * copyGPUinplace / copyGPUinplaceTypeCasted and the CopyInplaceGPU kernels
+ * (Matrix.mm:1699-1976, Copy.metal:14-80). */
+int mx_launch_copy_strided(int dst_dtype, int src_dtype, int cdims, const uint32_t* shape,
+                           const uint32_t* sDst, const uint32_t* sSrc,
+                           void* dst, const void* src, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MATRIX_AMD_H */

@@ -1,0 +1,297 @@
+"""matrix_amd -- MI355X (gfx950) evaluation path of the `matrix` lazy tensor library.
+
+This package is a thin ctypes view of the C launch ABI (include/matrix_amd.h) and of the host
+shape helpers (include/matrix_amd_shape.h), both exported by the in-tree library
+`matrix_amd/_lib/libmatrix_amd.so`.  There is no fallback: importing fails if the library
+has not been built (`python -m matrix_amd.build`).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("MATRIX_AMD_LIB", _PKG / "_lib" / "libmatrix_amd.so"))
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"matrix_amd: native library {LIB_PATH} is missing; build it with `python -m matrix_amd.build`"
+    )
+
+lib = ctypes.CDLL(str(LIB_PATH))
+
+# ------------------------------------------------------------------ codes (include/matrix_amd.h)
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_NOT_INITIALIZED, ERR_WORKSPACE = range(6)
+
+FLOAT32, FLOAT16, UINT8, INT32, INT16, UINT32, UINT16, BOOL, INT8, COMPLEX64, BFLOAT16, INT64, UINT64 = range(13)
+OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_EQ = range(7)
+RED_SUM, RED_MAX, RED_MIN, RED_ARGMAX, RED_ARGMIN = range(5)
+MAX_DIMS = 8
+
+# numpy storage dtype of every element code (16-bit floats stored as raw bits for bfloat16)
+NP_DTYPE = {
+    FLOAT32: np.float32, FLOAT16: np.float16, UINT8: np.uint8, INT32: np.int32, INT16: np.int16,
+    UINT32: np.uint32, UINT16: np.uint16, BOOL: np.bool_, INT8: np.int8, BFLOAT16: np.uint16,
+    INT64: np.int64, UINT64: np.uint64,
+}
+DTYPE_NAME = {
+    FLOAT32: "f32", FLOAT16: "f16", UINT8: "u8", INT32: "i32", INT16: "i16", UINT32: "u32",
+    UINT16: "u16", BOOL: "bool", INT8: "i8", BFLOAT16: "bf16", INT64: "i64", UINT64: "u64",
+}
+
+
+class MatrixAMDError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[mx status {status}] {message}")
+        self.status = status
+
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_i = ctypes.c_int
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_ip = ctypes.POINTER(ctypes.c_int)
+
+_SIGS = {
+    "mx_last_error": ([], ctypes.c_char_p),
+    "mx_version": ([], ctypes.c_char_p),
+    "mx_hip_init": ([_i], _i),
+    "mx_hip_shutdown": ([], _i),
+    "mx_hip_device_count": ([_ip], _i),
+    "mx_hip_alloc": ([_sz, ctypes.POINTER(_vp)], _i),
+    "mx_hip_free": ([_vp], _i),
+    "mx_hip_h2d": ([_vp, _vp, _sz, _vp], _i),
+    "mx_hip_d2h": ([_vp, _vp, _sz, _vp], _i),
+    "mx_hip_d2d": ([_vp, _vp, _sz, _vp], _i),
+    "mx_hip_memset": ([_vp, _i, _sz, _vp], _i),
+    "mx_hip_stream_for_thread": ([ctypes.POINTER(_vp)], _i),
+    "mx_hip_sync": ([_vp], _i),
+    "mx_hip_event_create": ([ctypes.POINTER(_vp)], _i),
+    "mx_hip_event_destroy": ([_vp], _i),
+    "mx_hip_event_record": ([_vp, _vp], _i),
+    "mx_hip_event_elapsed_ms": ([_vp, _vp, ctypes.POINTER(ctypes.c_float)], _i),
+    "mx_launch_bcast_binary": ([_i, _i, _i, _u32p, _u32p, _u32p, _u32p, _vp, _vp, _vp, _vp], _i),
+    "mx_reduce_workspace_bytes": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, ctypes.POINTER(_sz)], _i),
+    "mx_launch_reduce": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp, _sz, _vp], _i),
+    "mx_collapse_dims3": ([_u32p, _u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
+    "mx_collapse_dims2": ([_u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p], _i),
+    "mx_collapse_dims_matmul": ([_u32p, _u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
+    "mx_collapse_dims_reduce2": ([_u32p, _u32p, _u32p, _u32, _i, _i, _i, _u64, _u32p, _u32p, _u32p, _u32p], _i),
+    "mx_broadcast_shapes": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
+    "mx_broadcast_shapes_matmul": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
+}
+_OPTIONAL = {"mx_launch_batched_matmul", "mx_launch_conv_nd", "mx_conv_workspace_bytes", "mx_launch_copy_strided"}
+
+for _name, (_args, _res) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.argtypes = _args
+    _f.restype = _res
+
+if hasattr(lib, "mx_launch_batched_matmul"):
+    lib.mx_launch_batched_matmul.argtypes = [_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp]
+    lib.mx_launch_batched_matmul.restype = _i
+if hasattr(lib, "mx_conv_workspace_bytes"):
+    lib.mx_conv_workspace_bytes.argtypes = [_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _i, ctypes.POINTER(_sz)]
+    lib.mx_conv_workspace_bytes.restype = _i
+if hasattr(lib, "mx_launch_conv_nd"):
+    lib.mx_launch_conv_nd.argtypes = [_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _ip, _ip, _ip, _ip,
+                                      _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]
+    lib.mx_launch_conv_nd.restype = _i
+if hasattr(lib, "mx_launch_copy_strided"):
+    lib.mx_launch_copy_strided.argtypes = [_i, _i, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp]
+    lib.mx_launch_copy_strided.restype = _i
+
+
+def last_error() -> str:
+    msg = lib.mx_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise MatrixAMDError(status, last_error())
+
+
+def u32(seq) -> ctypes.Array:
+    """uint32 ctypes array (at least one slot so a pointer is always valid)."""
+    vals = [int(v) for v in seq]
+    arr = (ctypes.c_uint32 * max(1, len(vals)))(*vals)
+    return arr
+
+
+def i32(seq) -> ctypes.Array:
+    vals = [int(v) for v in seq]
+    return (ctypes.c_int * max(1, len(vals)))(*vals)
+
+
+# ------------------------------------------------------------------ device runtime
+_initialized = False
+
+
+def init(device: int = 0) -> None:
+    global _initialized
+    if not _initialized:
+        check(lib.mx_hip_init(device))
+        _initialized = True
+
+
+def sync(stream=None) -> None:
+    check(lib.mx_hip_sync(stream))
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    check(lib.mx_hip_device_count(ctypes.byref(n)))
+    return n.value
+
+
+class DeviceBuffer:
+    """An owned device allocation (mx_hip_alloc / mx_hip_free)."""
+
+    def __init__(self, nbytes: int):
+        init()
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        check(lib.mx_hip_alloc(self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value or 0
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray) -> "DeviceBuffer":
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes)
+        if arr.nbytes:
+            check(lib.mx_hip_h2d(buf.ptr, arr.ctypes.data, arr.nbytes, None))
+        return buf
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        if arr.nbytes:
+            check(lib.mx_hip_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes, None))
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dt.itemsize
+        out = np.empty(count, dtype=dt)
+        if out.nbytes:
+            assert offset + out.nbytes <= self.nbytes
+            check(lib.mx_hip_d2h(out.ctypes.data, self.ptr + offset, out.nbytes, None))
+        return out
+
+    def fill_bytes(self, value: int) -> None:
+        check(lib.mx_hip_memset(self.ptr, value, self.nbytes, None))
+
+    def free(self) -> None:
+        if self.ptr:
+            lib.mx_hip_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(lib.mx_hip_event_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def record(self, stream=None) -> None:
+        check(lib.mx_hip_event_record(self.ptr, stream))
+
+    def elapsed_ms(self, later: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib.mx_hip_event_elapsed_ms(self.ptr, later.ptr, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib.mx_hip_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ host shape helpers
+def _out_arrays(n=4):
+    return [(ctypes.c_uint32 * MAX_DIMS)() for _ in range(n)]
+
+
+def collapse_dims3(shape, sA, sB, sC, size_cap=2**31 - 1):
+    o = _out_arrays(4)
+    nd = ctypes.c_uint32()
+    check(lib.mx_collapse_dims3(u32(shape), u32(sA), u32(sB), u32(sC), len(shape), size_cap, *o, ctypes.byref(nd)))
+    n = nd.value
+    return [list(a[:n]) for a in o]
+
+
+def collapse_dims2(shape, sA, sB, size_cap=2**31 - 1):
+    o = _out_arrays(3)
+    nd = ctypes.c_uint32()
+    check(lib.mx_collapse_dims2(u32(shape), u32(sA), u32(sB), len(shape), size_cap, *o, ctypes.byref(nd)))
+    n = nd.value
+    return [list(a[:n]) for a in o]
+
+
+def collapse_dims_matmul(shape, sA, sB, sC, size_cap=2**31 - 1):
+    o = _out_arrays(4)
+    nd = ctypes.c_uint32()
+    check(lib.mx_collapse_dims_matmul(u32(shape), u32(sA), u32(sB), u32(sC), len(shape), size_cap, *o,
+                                      ctypes.byref(nd)))
+    n = nd.value
+    return [list(a[:n]) for a in o]
+
+
+def collapse_dims_reduce2(shape, sOut, sIn, axis, keep_dims=False, outer_collapsed=True, size_cap=2**32 - 1):
+    o = _out_arrays(3)
+    nd = ctypes.c_uint32()
+    check(lib.mx_collapse_dims_reduce2(u32(shape), u32(sOut), u32(sIn), len(shape), axis, int(keep_dims),
+                                       int(outer_collapsed), size_cap, *o, ctypes.byref(nd)))
+    n = nd.value
+    return [list(a[:n]) for a in o]
+
+
+def broadcast_shapes(shape1, strides1, shape2, strides2, matmul=False):
+    o = _out_arrays(6)
+    fn = lib.mx_broadcast_shapes_matmul if matmul else lib.mx_broadcast_shapes
+    check(fn(u32(shape1), u32(strides1), len(shape1), u32(shape2), u32(strides2), len(shape2), *o))
+    n = max(len(shape1), len(shape2))
+    return [list(a[:n]) for a in o]
+
+
+def contiguous_strides(shape):
+    st, acc = [0] * len(shape), 1
+    for i in range(len(shape) - 1, -1, -1):
+        st[i] = acc
+        acc *= int(shape[i])
+    return st
+
+
+# ------------------------------------------------------------------ kernel launches
+def launch_bcast_binary(op, dtype, desc, R, A, B, stream=None):
+    shape, sA, sB, sR = desc
+    check(lib.mx_launch_bcast_binary(op, dtype, len(shape), u32(shape), u32(sR), u32(sA), u32(sB),
+                                     int(R), int(A), int(B), stream))
+
+
+def reduce_workspace_bytes(op, dtype, reduce_stride, n_reduce, desc):
+    shape, sOut, sIn = desc
+    nb = ctypes.c_size_t()
+    check(lib.mx_reduce_workspace_bytes(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut),
+                                        u32(sIn), ctypes.byref(nb)))
+    return nb.value
+
+
+def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=0, workspace_bytes=0,
+                  stream=None):
+    shape, sOut, sIn = desc
+    check(lib.mx_launch_reduce(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn),
+                               int(out), int(inp), int(workspace), workspace_bytes, stream))

@@ -1,0 +1,101 @@
+"""Builds the gfx950 kernel library (and the oracle when asked) in-tree.
+
+    python -m matrix_amd.build            # kernels -> matrix_amd/_lib/libmatrix_amd.so
+    python -m matrix_amd.build --oracle   # also oracle/_build/liboracle.so
+
+Objects are compiled in parallel with hipcc for gfx950 only; packed-fp32 instructions are
+disabled for all device code.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+OBJ = PKG / "_build"
+LIBDIR = PKG / "_lib"
+LIB = LIBDIR / "libmatrix_amd.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{ROOT / 'include'}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}")
+    # hipcc's host pass warns that it does not know the packed-fp32 feature; drop that line
+    noise = [ln for ln in (proc.stdout + proc.stderr).splitlines()
+             if ln.strip() and "packed-fp32-ops" not in ln and "is not a recognized feature" not in ln]
+    if noise:
+        sys.stderr.write("\n".join(noise) + "\n")
+
+
+CXX = os.environ.get("MX_CXX", "/opt/rocm/llvm/bin/clang++")
+HOST = PKG / "host"
+CXX_FLAGS = ["-std=c++23", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
+             f"-I{ROOT / 'include'}"]
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def host_sources() -> list[Path]:
+    return sorted(HOST.glob("*.cpp"))
+
+
+def build_kernels(jobs: int | None = None) -> Path:
+    OBJ.mkdir(exist_ok=True)
+    LIBDIR.mkdir(exist_ok=True)
+    srcs = sources()
+    hsrcs = host_sources()
+    cmds = [[HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(OBJ / (s.stem + ".o"))] for s in srcs]
+    cmds += [[CXX, *CXX_FLAGS, "-c", str(s), "-o", str(OBJ / ("host_" + s.stem + ".o"))] for s in hsrcs]
+    objs = [OBJ / (s.stem + ".o") for s in srcs] + [OBJ / ("host_" + s.stem + ".o") for s in hsrcs]
+    jobs = jobs or min(len(cmds), os.cpu_count() or 4, 8)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_run, c) for c in cmds]
+        for f in futs:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+    return ROOT / "oracle" / "_build" / "liboracle.so"
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--oracle", action="store_true", help="also build the CPU oracle")
+    ap.add_argument("-j", type=int, default=None)
+    a = ap.parse_args(argv)
+    print(build_kernels(a.j))
+    if a.oracle:
+        print(build_oracle())
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,256 @@
+// bcast.hip -- broadcast binary kernels: Add / Sub / Mul / Divide / Max / Min / Equal.
+//
+// Semantics per element follow the reference CPU backends (Matrix.mm:7411-7707,
+// Matrix.mm:13378-13478, Matrix.mm:14668-14783, Matrix.mm:14469-14540):
+//   - 16-bit floats compute in float and round once (nearest-even) on store;
+//   - integers wrap; integer division truncates, a zero divisor gives 0 and MIN / -1 gives
+//     MIN (arm64 sdiv / udiv, the reference's platform);
+//   - Max is (a < b) ? b : a and Min is (b < a) ? b : a, selecting the operand's own bits
+//     (std::max / std::min), so NaN and signed-zero ties resolve as on the CPU;
+//   - Equal writes 1 / 0 in the operands' dtype.
+//
+// Layout: the iteration space is the collapsed CollapsedDims_3 of collapse_dims
+// (Mods/Utils.mm:169-202).  When the innermost collapsed axis is unit-stride in the output
+// and unit- or zero-stride in each operand, one thread moves 16 bytes per operand with
+// 128-bit loads and stores; otherwise a scalar kernel gathers with the full strides.
+#include "common.hpp"
+
+namespace mx {
+namespace {
+
+template <int DT, int OP>
+struct BinOp {
+    using Tr = dt_traits<DT>;
+    using S = typename Tr::S;
+    __device__ __forceinline__ static S apply(S a, S b) {
+        if constexpr (Tr::is_float) {
+            float x = Tr::ld(a), y = Tr::ld(b);
+            if constexpr (OP == MX_OP_ADD) return Tr::st(x + y);
+            else if constexpr (OP == MX_OP_SUB) return Tr::st(x - y);
+            else if constexpr (OP == MX_OP_MUL) return Tr::st(x * y);
+            else if constexpr (OP == MX_OP_DIV) return Tr::st(x / y);
+            else if constexpr (OP == MX_OP_MAX) return (x < y) ? b : a;
+            else if constexpr (OP == MX_OP_MIN) return (y < x) ? b : a;
+            else return (x == y) ? Tr::st(1.0f) : Tr::st(0.0f);
+        } else if constexpr (DT == MX_BOOL) {
+            int x = a, y = b;
+            if constexpr (OP == MX_OP_ADD) return (S)((x + y) != 0);
+            else if constexpr (OP == MX_OP_SUB) return (S)((x - y) != 0);
+            else if constexpr (OP == MX_OP_MUL) return (S)((x * y) != 0);
+            else if constexpr (OP == MX_OP_DIV) return (S)(y == 0 ? 0 : ((x / y) != 0));
+            else if constexpr (OP == MX_OP_MAX) return (x < y) ? b : a;
+            else if constexpr (OP == MX_OP_MIN) return (y < x) ? b : a;
+            else return (S)(x == y ? 1 : 0);
+        } else {
+            // wrap-around arithmetic in an unsigned type at least 32 bits wide
+            using U = std::conditional_t<(sizeof(S) <= 4), uint32_t, uint64_t>;
+            if constexpr (OP == MX_OP_ADD) return (S)((U)a + (U)b);
+            else if constexpr (OP == MX_OP_SUB) return (S)((U)a - (U)b);
+            else if constexpr (OP == MX_OP_MUL) return (S)((U)a * (U)b);
+            else if constexpr (OP == MX_OP_DIV) {
+                if (b == 0) return (S)0;
+                if constexpr (Tr::is_signed) {
+                    using W = std::conditional_t<(sizeof(S) <= 4), int32_t, int64_t>;
+                    W x = a, y = b;
+                    if (y == -1) return (S)(0 - (U)x);      // MIN / -1 wraps to MIN
+                    return (S)(x / y);
+                } else {
+                    return (S)((U)a / (U)b);
+                }
+            } else if constexpr (OP == MX_OP_MAX) return (a < b) ? b : a;
+            else if constexpr (OP == MX_OP_MIN) return (b < a) ? b : a;
+            else return (S)(a == b ? 1 : 0);
+        }
+    }
+};
+
+constexpr int kMaxOuter = MX_MAX_DIMS - 1;
+
+struct OuterDesc {                  // outer (non-innermost) collapsed axes
+    int n;                          // number of outer axes
+    FastDiv shape[kMaxOuter];
+    uint32_t sA[kMaxOuter], sB[kMaxOuter], sR[kMaxOuter];
+};
+
+struct FullDesc {                   // all collapsed axes
+    int n;
+    FastDiv shape[MX_MAX_DIMS];
+    uint32_t sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sR[MX_MAX_DIMS];
+};
+
+template <typename S, int VEC>
+struct alignas(16) Vec { S v[VEC]; };
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 2;
+
+// One thread = kUnroll slots of VEC consecutive outputs along the innermost axis.
+template <int DT, int OP, int VEC, bool AV, bool BV>
+__global__ __launch_bounds__(kBlock) void bcast_vec_kernel(
+    typename dt_traits<DT>::S* __restrict__ R, const typename dt_traits<DT>::S* __restrict__ A,
+    const typename dt_traits<DT>::S* __restrict__ B, uint32_t nvec, FastDiv inner_vecs,
+    OuterDesc od) {
+    using S = typename dt_traits<DT>::S;
+    using V = Vec<S, VEC>;
+    const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    V va[kUnroll], vb[kUnroll];
+    uint64_t offR[kUnroll];
+    bool live[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        const uint32_t v = base + u * kBlock;
+        live[u] = v < nvec;
+        if (!live[u]) continue;
+        uint32_t row = inner_vecs.div(v);
+        uint32_t col = (v - row * inner_vecs.d) * VEC;
+        uint64_t oa = 0, ob = 0, orr = 0;
+        for (int d = od.n - 1; d >= 0; --d) {
+            uint32_t q = od.shape[d].div(row);
+            uint32_t idx = row - q * od.shape[d].d;
+            row = q;
+            oa += (uint64_t)idx * od.sA[d];
+            ob += (uint64_t)idx * od.sB[d];
+            orr += (uint64_t)idx * od.sR[d];
+        }
+        offR[u] = orr + col;
+        if constexpr (AV) va[u] = *reinterpret_cast<const V*>(A + oa + col);
+        else { S s = A[oa];
+#pragma unroll
+            for (int i = 0; i < VEC; i++) va[u].v[i] = s; }
+        if constexpr (BV) vb[u] = *reinterpret_cast<const V*>(B + ob + col);
+        else { S s = B[ob];
+#pragma unroll
+            for (int i = 0; i < VEC; i++) vb[u].v[i] = s; }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        if (!live[u]) continue;
+        V r;
+#pragma unroll
+        for (int i = 0; i < VEC; i++) r.v[i] = BinOp<DT, OP>::apply(va[u].v[i], vb[u].v[i]);
+        *reinterpret_cast<V*>(R + offR[u]) = r;
+    }
+}
+
+// Scalar gather: one output element per thread, any strides.
+template <int DT, int OP>
+__global__ __launch_bounds__(kBlock) void bcast_scalar_kernel(
+    typename dt_traits<DT>::S* __restrict__ R, const typename dt_traits<DT>::S* __restrict__ A,
+    const typename dt_traits<DT>::S* __restrict__ B, uint32_t total, FullDesc fd) {
+    uint32_t g = blockIdx.x * kBlock + threadIdx.x;
+    if (g >= total) return;
+    uint32_t rem = g;
+    uint64_t oa = 0, ob = 0, orr = 0;
+    for (int d = fd.n - 1; d >= 0; --d) {
+        uint32_t q = fd.shape[d].div(rem);
+        uint32_t idx = rem - q * fd.shape[d].d;
+        rem = q;
+        oa += (uint64_t)idx * fd.sA[d];
+        ob += (uint64_t)idx * fd.sB[d];
+        orr += (uint64_t)idx * fd.sR[d];
+    }
+    R[orr] = BinOp<DT, OP>::apply(A[oa], B[ob]);
+}
+
+template <int DT, int OP>
+int launch_typed(int cdims, const uint32_t* shape, const uint32_t* sR, const uint32_t* sA,
+                 const uint32_t* sB, void* Rp, const void* Ap, const void* Bp, uint64_t total,
+                 hipStream_t st) {
+    using S = typename dt_traits<DT>::S;
+    S* R = (S*)Rp;
+    const S* A = (const S*)Ap;
+    const S* B = (const S*)Bp;
+    constexpr int VEC = 16 / sizeof(S);
+    if (cdims == 0) {
+        FullDesc fd{};
+        fd.n = 0;
+        hipLaunchKernelGGL((bcast_scalar_kernel<DT, OP>), dim3(1), dim3(kBlock), 0, st, R, A, B, 1u, fd);
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    }
+    const int in = cdims - 1;
+    const uint32_t inner = shape[in];
+    bool vec = (VEC > 1) && sR[in] == 1 && (sA[in] <= 1) && (sB[in] <= 1) && (inner % VEC == 0) &&
+               (sA[in] == 1 || sB[in] == 1) && ((uintptr_t)R % 16 == 0);
+    if (vec && sA[in] == 1 && (uintptr_t)A % 16 != 0) vec = false;
+    if (vec && sB[in] == 1 && (uintptr_t)B % 16 != 0) vec = false;
+    for (int d = 0; vec && d < in; d++) {
+        if (sR[d] % VEC) vec = false;
+        if (sA[in] == 1 && sA[d] % VEC) vec = false;
+        if (sB[in] == 1 && sB[d] % VEC) vec = false;
+    }
+    if (vec) {
+        OuterDesc od{};
+        od.n = in;
+        for (int d = 0; d < in; d++) {
+            od.shape[d] = FastDiv(shape[d]);
+            od.sA[d] = sA[d]; od.sB[d] = sB[d]; od.sR[d] = sR[d];
+        }
+        uint32_t nvec = (uint32_t)(total / VEC);
+        dim3 grid((nvec + kBlock * kUnroll - 1) / (kBlock * kUnroll));
+        FastDiv iv(inner / VEC);
+        if (sA[in] == 1 && sB[in] == 1)
+            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, true, true>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od);
+        else if (sA[in] == 1)
+            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, true, false>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od);
+        else
+            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, false, true>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od);
+    } else {
+        FullDesc fd{};
+        fd.n = cdims;
+        for (int d = 0; d < cdims; d++) {
+            fd.shape[d] = FastDiv(shape[d]);
+            fd.sA[d] = sA[d]; fd.sB[d] = sB[d]; fd.sR[d] = sR[d];
+        }
+        dim3 grid((uint32_t)((total + kBlock - 1) / kBlock));
+        hipLaunchKernelGGL((bcast_scalar_kernel<DT, OP>), grid, dim3(kBlock), 0, st, R, A, B, (uint32_t)total, fd);
+    }
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
+template <int DT>
+int launch_op(int op, int cdims, const uint32_t* shape, const uint32_t* sR, const uint32_t* sA,
+              const uint32_t* sB, void* R, const void* A, const void* B, uint64_t total, hipStream_t st) {
+    switch (op) {
+    case MX_OP_ADD: return launch_typed<DT, MX_OP_ADD>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    case MX_OP_SUB: return launch_typed<DT, MX_OP_SUB>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    case MX_OP_MUL: return launch_typed<DT, MX_OP_MUL>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    case MX_OP_DIV: return launch_typed<DT, MX_OP_DIV>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    case MX_OP_MAX: return launch_typed<DT, MX_OP_MAX>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    case MX_OP_MIN: return launch_typed<DT, MX_OP_MIN>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    case MX_OP_EQ: return launch_typed<DT, MX_OP_EQ>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+    default: return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: unknown op " + std::to_string(op));
+    }
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_launch_bcast_binary(int op, int dtype, int cdims, const uint32_t* shape,
+                                      const uint32_t* sR, const uint32_t* sA, const uint32_t* sB,
+                                      void* R, const void* A, const void* B, void* stream) {
+    if (cdims < 0 || cdims > MX_MAX_DIMS)
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: cdims " + std::to_string(cdims) + " outside [0, 8]");
+    if (cdims > 0 && (!shape || !sR || !sA || !sB))
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: null descriptor");
+    if (op < MX_OP_ADD || op > MX_OP_EQ)
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: unknown op " + std::to_string(op));
+    uint64_t total = 1;
+    for (int d = 0; d < cdims; d++) total *= shape[d];
+    if (total == 0) return MX_OK;
+    if (total > 0xffffffffull)
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: more than 2^32-1 elements (size_m indexing)");
+    if (!R || !A || !B) return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: null buffer");
+    hipStream_t st;
+    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+    int rc = MX_OK;
+    bool ok = dispatch_dtype(dtype, [&](auto dt) {
+        rc = launch_op<decltype(dt)::value>(op, cdims, shape, sR, sA, sB, R, A, B, total, st);
+    });
+    if (!ok)
+        return fail(MX_ERR_UNSUPPORTED, "mx_launch_bcast_binary: no kernel for dtype " + std::to_string(dtype));
+    return rc;
+}

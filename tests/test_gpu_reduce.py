@@ -1,0 +1,233 @@
+"""GPU parity: Sum / Max / Min / ArgMax / ArgMin vs the oracle.
+
+Max / Min / ArgMax / ArgMin and integer sums are bit-exact; fp32 sums satisfy
+|gpu - cpu| <= 1e-4 * sum|x| per output (and normwise <= 1e-4); 16-bit float sums are
+checked against the oracle's fp32-accumulator mode (one rounding at the end).
+"""
+import numpy as np
+import pytest
+
+from helpers import bits, contiguous_strides, normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+SUM_TOL = 1e-4
+
+
+def reduce_desc(mx, shape, axis, in_strides=None, keepdims=False):
+    in_strides = in_strides or contiguous_strides(shape)
+    if keepdims:
+        out_shape = [1 if i == axis else s for i, s in enumerate(shape)]
+    else:
+        out_shape = [s for i, s in enumerate(shape) if i != axis]
+    desc = mx.collapse_dims_reduce2(shape, contiguous_strides(out_shape), in_strides, axis,
+                                    keep_dims=False, outer_collapsed=not keepdims)
+    total = int(np.prod(out_shape)) if out_shape else 1
+    return desc, in_strides[axis], shape[axis], total
+
+
+def run_reduce(mx, orc, op, code, x_flat, shape, axis, in_strides=None, keepdims=False, acc=None):
+    desc, rs, n, total = reduce_desc(mx, shape, axis, in_strides, keepdims)
+    X = mx.DeviceBuffer(max(x_flat.nbytes, 16))
+    X.upload(x_flat.view(np.uint8))
+    out_dt = np.int32 if op in (mx.RED_ARGMAX, mx.RED_ARGMIN) else x_flat.dtype
+    O = mx.DeviceBuffer(max(total, 1) * np.dtype(out_dt).itemsize)
+    wsb = mx.reduce_workspace_bytes(op, code, rs, n, desc)
+    W = mx.DeviceBuffer(wsb) if wsb else None
+    mx.launch_reduce(op, code, rs, n, desc, O.ptr, X.ptr, W.ptr if W else 0, wsb)
+    mx.sync()
+    got = O.download(out_dt, total)
+    ref = orc.reduce(op, code, rs, n, desc, total, x_flat, acc=orc.ACC_F32 if acc is None else acc)
+    return got, ref, desc, rs, n
+
+
+def check_sum(got, ref, x_abs_sum):
+    g = got.astype(np.float64)
+    r = ref.astype(np.float64)
+    assert np.all(np.abs(g - r) <= SUM_TOL * np.maximum(x_abs_sum, 1e-30) + 1e-30)
+    assert normwise_rel(g, r) <= SUM_TOL
+
+
+def abs_sum(mx, x_flat, shape, axis, in_strides=None):
+    in_strides = in_strides or contiguous_strides(shape)
+    view = np.lib.stride_tricks.as_strided(x_flat.astype(np.float64),
+                                           shape=shape, strides=[s * 8 for s in in_strides])
+    return np.abs(view).sum(axis).ravel()
+
+
+def inject_ties(rng, x, axis, frac=0.3, minimum=False):
+    """Copy each chosen row's extremum to 1-3 more random positions (30% of rows)."""
+    xm = np.moveaxis(x, axis, -1)
+    rows = xm.reshape(-1, xm.shape[-1])
+    for r in np.nonzero(rng.random(rows.shape[0]) < frac)[0]:
+        v = rows[r].min() if minimum else rows[r].max()
+        rows[r, rng.integers(0, rows.shape[1], rng.integers(1, 4))] = v
+    return np.ascontiguousarray(np.moveaxis(rows.reshape(xm.shape), -1, axis))
+
+
+OPS = ["RED_SUM", "RED_MAX", "RED_MIN", "RED_ARGMAX", "RED_ARGMIN"]
+
+
+@pytest.mark.parametrize("axis", [1, 0])
+@pytest.mark.parametrize("opn", OPS)
+def test_reductions_256x65536(mx, orc, axis, opn):
+    """X[256,65536] ~ N(0,1), seed 0, 30% of rows with duplicated extrema (the reductions workload)."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal([256, 65536]).astype(np.float32)
+    x = inject_ties(rng, x, axis, minimum=op in (mx.RED_MIN, mx.RED_ARGMIN))
+    got, ref, *_ = run_reduce(mx, orc, op, mx.FLOAT32, x.ravel(), [256, 65536], axis)
+    if op == mx.RED_SUM:
+        check_sum(got, ref, np.abs(x.astype(np.float64)).sum(axis))
+    else:
+        assert np.array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize("opn", OPS)
+def test_reshaped_chain_axes_3_then_1(mx, orc, opn):
+    """X.reshape(64,4,4096,16) reduced over axis 3, then axis 1 (the non-contiguous split)."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal([64, 4, 4096, 16]).astype(np.float32)
+    got3, ref3, desc, *_ = run_reduce(mx, orc, op, mx.FLOAT32, x.ravel(), [64, 4, 4096, 16], 3)
+    assert desc == [[1048576], [1], [16]]
+    if op == mx.RED_SUM:
+        check_sum(got3, ref3, np.abs(x.astype(np.float64)).sum(3).ravel())
+    else:
+        assert np.array_equal(bits(got3), bits(ref3))
+    if op in (mx.RED_ARGMAX, mx.RED_ARGMIN):
+        # arg-reductions take one axis: run axis 1 of the original tensor's [64,4,4096] slice
+        y = np.ascontiguousarray(x[..., 0])
+    else:
+        y = got3.reshape(64, 4, 4096)
+    got1, ref1, desc1, *_ = run_reduce(mx, orc, op, mx.FLOAT32, y.ravel(), [64, 4, 4096], 1)
+    assert desc1 == [[64, 4096], [4096, 1], [16384, 1]]
+    if op == mx.RED_SUM:
+        check_sum(got1, ref1, np.abs(y.astype(np.float64)).sum(1).ravel())
+    else:
+        assert np.array_equal(bits(got1), bits(ref1))
+
+
+def test_add_rowsum_sum(mx, orc):
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal([4096, 1024]).astype(np.float32)
+    b = rng.uniform(-1, 1, [1, 1024]).astype(np.float32)
+    c = (a + b).astype(np.float32)
+    got, ref, *_ = run_reduce(mx, orc, mx.RED_SUM, mx.FLOAT32, c.ravel(), [4096, 1024], 1)
+    check_sum(got, ref, np.abs(c.astype(np.float64)).sum(1))
+
+
+@pytest.mark.parametrize("shape,axis", [([3, 5], 1), ([7, 2], 1), ([9, 40], 1), ([11, 200], 1), ([5, 3000], 1),
+                                        ([2, 50000], 1), ([37, 53], 0), ([4, 5, 6, 7], 2), ([4, 5, 6, 7], 0),
+                                        ([1, 1], 0), ([6, 1, 8], 1), ([3, 4, 5], 2)])
+@pytest.mark.parametrize("opn", OPS)
+def test_plans_f32(mx, orc, shape, axis, opn):
+    """Covers every plan: L-lane rows, block + finalize, columns with and without chunks."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(2)
+    x = np.round(rng.standard_normal(shape) * 3).astype(np.float32)   # many ties and +-0
+    x[rng.random(shape) < 0.1] *= -0.0
+    got, ref, *_ = run_reduce(mx, orc, op, mx.FLOAT32, x.ravel(), shape, axis)
+    if op == mx.RED_SUM:
+        check_sum(got, ref, abs_sum(mx, x.ravel(), shape, axis))
+    else:
+        assert np.array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize("keepdims", [False, True])
+def test_keepdims_and_strided_input(mx, orc, keepdims):
+    rng = np.random.default_rng(3)
+    base = rng.standard_normal([24, 36]).astype(np.float32)
+    # transposed view [36, 24] with strides [1, 36]
+    for op in (mx.RED_MAX, mx.RED_ARGMIN, mx.RED_SUM):
+        for axis in (0, 1):
+            got, ref, *_ = run_reduce(mx, orc, op, mx.FLOAT32, base.ravel(), [36, 24], axis, in_strides=[1, 36],
+                                      keepdims=keepdims)
+            if op == mx.RED_SUM:
+                check_sum(got, ref, np.abs(base.T.astype(np.float64)).sum(axis).ravel())
+            else:
+                assert np.array_equal(bits(got), bits(ref))
+
+
+def test_special_rows(mx, orc):
+    nan, inf = np.nan, np.inf
+    rows = np.full([8, 1000], -inf, np.float32)
+    rows[1, 500] = nan
+    rows[2, :] = nan
+    rows[2, 999] = -3.0
+    rows[3, :] = 0.0
+    rows[3, 7] = -0.0
+    rows[4, :] = -0.0
+    rows[4, 900] = 0.0
+    rows[5, ::3] = 5.0
+    rows[6, :] = -3.4028234663852886e38
+    rows[7, :] = np.linspace(-1, 1, 1000, dtype=np.float32)
+    for op in (mx.RED_MAX, mx.RED_MIN, mx.RED_ARGMAX, mx.RED_ARGMIN):
+        for x in (rows, -rows):
+            got, ref, *_ = run_reduce(mx, orc, op, mx.FLOAT32, np.ascontiguousarray(x).ravel(), [8, 1000], 1)
+            assert np.array_equal(bits(got), bits(ref)), op
+            gotc, refc, *_ = run_reduce(mx, orc, op, mx.FLOAT32, np.ascontiguousarray(x.T).ravel(), [1000, 8], 0)
+            assert np.array_equal(bits(gotc), bits(refc)), op
+
+
+INT_DTYPES = ["INT32", "INT8", "INT16", "INT64", "UINT8", "UINT16", "UINT32", "UINT64", "BOOL"]
+
+
+@pytest.mark.parametrize("dt", INT_DTYPES)
+@pytest.mark.parametrize("opn", OPS)
+def test_integer_dtypes_exact(mx, orc, dt, opn):
+    code, op = getattr(mx, dt), getattr(mx, opn)
+    npt = mx.NP_DTYPE[code]
+    rng = np.random.default_rng(4)
+    for shape, axis in [([16, 700], 1), ([300, 40], 0), ([5, 9000], 1)]:
+        if code == mx.BOOL:
+            x = rng.integers(0, 2, size=shape).astype(np.bool_)
+        else:
+            info = np.iinfo(npt)
+            x = rng.integers(info.min, info.max, size=shape, dtype=npt, endpoint=True)
+        got, ref, *_ = run_reduce(mx, orc, op, code, x.ravel(), shape, axis)
+        assert np.array_equal(bits(got), bits(ref)), (dt, opn, shape, axis)
+
+
+@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("opn", OPS)
+def test_half_dtypes(mx, orc, dt, opn):
+    code, op = getattr(mx, dt), getattr(mx, opn)
+    rng = np.random.default_rng(5)
+    for shape, axis in [([16, 4000], 1), ([300, 48], 0), ([8, 64], 1)]:
+        xf = np.round(rng.standard_normal(shape) * 8).astype(np.float32)
+        if code == mx.FLOAT16:
+            x = xf.astype(np.float16)
+        else:
+            from oracle.oracle import f32_to_bf16_bits
+            x = f32_to_bf16_bits(xf)
+        got, ref, *_ = run_reduce(mx, orc, op, code, x.ravel(), shape, axis)
+        if op == mx.RED_SUM:
+            g = got.astype(np.float32) if code == mx.FLOAT16 else (got.astype(np.uint32) << 16).view(np.float32)
+            r = ref.astype(np.float32) if code == mx.FLOAT16 else (ref.astype(np.uint32) << 16).view(np.float32)
+            # integer-valued inputs: fp32 partial sums are exact, so both round the same exact sum
+            assert np.array_equal(g, r)
+        else:
+            assert np.array_equal(bits(got), bits(ref))
+
+
+def test_empty_reduced_axis(mx, orc):
+    # shape[axis] == 0: sum 0, max -FLT_MAX, argmax 0, as the reference's empty loops give
+    desc = [[3], [1], [0]]
+    X = mx.DeviceBuffer(16)
+    for op, exp in [(mx.RED_SUM, [0.0] * 3), (mx.RED_MAX, [-3.4028234663852886e38] * 3), (mx.RED_ARGMAX, [0] * 3)]:
+        dt = np.int32 if op == mx.RED_ARGMAX else np.float32
+        O = mx.DeviceBuffer(12)
+        mx.launch_reduce(op, mx.FLOAT32, 1, 0, desc, O.ptr, X.ptr)
+        mx.sync()
+        assert O.download(dt, 3).tolist() == np.array(exp, dt).tolist()
+
+
+def test_workspace_too_small_is_an_error(mx):
+    desc = [[256], [1], [65536]]
+    nb = mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 65536, desc)
+    assert nb > 0
+    X = mx.DeviceBuffer(256 * 65536 * 4)
+    O = mx.DeviceBuffer(256 * 4)
+    with pytest.raises(mx.MatrixAMDError, match="workspace"):
+        mx.launch_reduce(mx.RED_SUM, mx.FLOAT32, 1, 65536, desc, O.ptr, X.ptr, 0, 0)
