@@ -98,9 +98,11 @@ int mx_launch_bcast_binary(int op, int dtype, int cdims, const uint32_t* shape,
  * max / min (Matrix.mm:14812-15059) and argmax / argmin (Matrix.mm:16182-16458).  The arrays
  * are exactly CollapsedDims_2 from collapse_dims_reduce (Mods/Utils.mm:321-376): shape,
  * stridesA (= sOut), stridesB (= sIn); reduce_stride / n_reduce are strides()[axis] and
- * shape()[axis] (Matrix.mm:15104-15105).  ARGMAX / ARGMIN write int32.  The workspace holds
- * the second pass's partials; its size comes from mx_reduce_workspace_bytes (0 is valid when
- * that returns 0). */
+ * shape()[axis] (Matrix.mm:15104-15105).  ARGMAX / ARGMIN write int32.  When the reduced axis
+ * is split over several blocks (few outputs, long axis), the workspace holds their partials and
+ * a second launch combines them; its size comes from mx_reduce_workspace_bytes (0 means none is
+ * needed, and then workspace may be NULL).  Launches that share one workspace must not overlap
+ * in time (use one stream). */
 int mx_reduce_workspace_bytes(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduce,
                               int cdims, const uint32_t* shape, const uint32_t* sOut,
                               const uint32_t* sIn, size_t* bytes);

@@ -10,14 +10,18 @@
 //   - integer sums wrap in the element type; 16-bit float sums accumulate in fp32.
 // Every partial carries the index it came from and the combine step breaks value ties by
 // the smaller index, so any split of the axis over lanes, waves and blocks reproduces the
-// sequential left-to-right result bit for bit.  fp32 sums are a tree (within tolerance).
+// sequential left-to-right result bit for bit.  fp32 sums are a fixed-shape tree
+// (deterministic run to run, within tolerance of the sequential sum).
 //
-// Plans (chosen on the host from the CollapsedDims_2 descriptor):
-//   rows    reduce stride 1: L lanes per output (L = 1, 4, 16, 64) with 128-bit loads;
-//   block   reduce stride 1, long rows: one 256-thread block per (output, chunk), chunks
-//           combined by a second pass (finalize);
-//   cols    reduce stride != 1: a thread owns VEC consecutive outputs and walks the axis,
-//           optionally split into chunks combined by finalize.
+// Plans, chosen on the host from the CollapsedDims_2 descriptor:
+//   rows   reduce stride 1, short or medium rows: L lanes per output (L = 1, 4, 16, 64),
+//          128-bit loads, several outputs in flight per lane group;
+//   block  reduce stride 1, long rows: one 256-thread block per (output, 32 KB chunk);
+//   cols   reduce stride != 1: a lane owns VEC consecutive outputs, the waves of a block
+//          split the reduced axis between them and combine through LDS.
+// The plans avoid splitting one output's axis over blocks whenever the outputs alone cover the
+// CUs; when they must split, each block writes its partial to the workspace and a second launch
+// combines the partials in split order.
 #include "common.hpp"
 
 #include <climits>
@@ -27,7 +31,6 @@
 namespace mx {
 namespace {
 
-constexpr int kBlock = 256;
 constexpr uint32_t kEmpty = 0x7fffffffu;   // index of a partial that took no element
 
 // ------------------------------------------------------------------ reduction states
@@ -58,12 +61,11 @@ template <int DT> struct Limits {
     }
 };
 
-// Sum state
-template <int DT, typename Enable = void> struct SumRed {
+// Sum state: float for 16/32-bit floats, wrap-around unsigned for integers, OR for bool.
+template <int DT> struct SumRed {
     using Tr = dt_traits<DT>;
     using S = typename Tr::S;
     using OutT = S;
-    // float for 16/32-bit floats, wrap-around unsigned for integers, OR for bool
     using St = std::conditional_t<Tr::is_float, float,
                std::conditional_t<(sizeof(S) <= 4), uint32_t, uint64_t>>;
     __device__ __forceinline__ static St init() { return St(0); }
@@ -126,7 +128,9 @@ template <int DT> struct RedSel<DT, MX_RED_ARGMAX> { using R = ExtRed<DT, true, 
 template <int DT> struct RedSel<DT, MX_RED_ARGMIN> { using R = ExtRed<DT, false, true>; };
 
 // ------------------------------------------------------------------ descriptors
-struct OffDesc {                       // offset of output g = sum_i (g / sOut_i ...) * sIn_i
+// Input offset of output g: the reference decomposes g with the collapsed output strides
+// (off = sum_i (rem / sOut_i) * sIn_i; rem %= sOut_i), Matrix.mm:15190-15194.
+struct OffDesc {
     int n;
     FastDiv so[MX_MAX_DIMS];
     uint32_t si[MX_MAX_DIMS];
@@ -142,153 +146,207 @@ struct OffDesc {                       // offset of output g = sum_i (g / sOut_i
     }
 };
 
-template <typename S, int VEC> struct alignas(VEC * sizeof(S) >= 16 ? 16 : VEC * sizeof(S)) VecT { S v[VEC]; };
+template <typename S, int VEC>
+struct alignas(VEC * sizeof(S) >= 16 ? 16 : VEC * sizeof(S)) VecT { S v[VEC]; };
 
-// ------------------------------------------------------------------ kernels
-// rows: L lanes per output, reduce stride 1.
-template <int DT, int OP, int VEC, int L>
-__global__ __launch_bounds__(kBlock) void reduce_rows_kernel(
+// Partials of a split axis are combined by reduce_finalize_kernel, a second launch on the same
+// stream.  (Combining them inside the first launch needs a device-scope release per block; on
+// this multi-XCD part that is an L2 write-back, which costs more than the extra launch.)
+
+// ------------------------------------------------------------------ rows (stride 1), L lanes per output
+// U outputs per lane group are in flight at once; every group runs the same number of rounds so
+// the group shuffles always see all of their lanes active.
+template <int DT, int OP, int VEC, int L, int U>
+__global__ __launch_bounds__(256) void reduce_rows_kernel(
     typename RedSel<DT, OP>::R::OutT* __restrict__ out, const typename dt_traits<DT>::S* __restrict__ in,
-    uint32_t total_out, uint32_t n, OffDesc od) {
-    using R = typename RedSel<DT, OP>::R;
-    using S = typename dt_traits<DT>::S;
-    using V = VecT<S, VEC>;
-    const uint64_t tid = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-    const uint32_t g = (uint32_t)(tid / L);
-    const uint32_t lane = (uint32_t)(tid % L);
-    typename R::St st = R::init();
-    if (g < total_out) {
-        const S* row = in + od.offset(g);
-        for (uint32_t e = lane * VEC; e < n; e += L * VEC) {
-            V v = *reinterpret_cast<const V*>(row + e);
-#pragma unroll
-            for (int k = 0; k < VEC; k++) R::step(st, v.v[k], e + k);
-        }
-    }
-#pragma unroll
-    for (int m = L / 2; m >= 1; m >>= 1) st = R::combine(st, R::shfl(st, m));
-    if (g < total_out && lane == 0) out[g] = R::out(st);
-}
-
-// block: one 256-thread block per (output, chunk); chunk partials go to the workspace.
-template <int DT, int OP, int VEC>
-__global__ __launch_bounds__(kBlock) void reduce_block_kernel(
-    typename RedSel<DT, OP>::R::OutT* __restrict__ out, typename RedSel<DT, OP>::R::St* __restrict__ ws,
-    const typename dt_traits<DT>::S* __restrict__ in, uint32_t total_out, uint32_t n,
-    uint32_t chunk, uint32_t nchunks, OffDesc od) {
+    uint32_t total_out, uint32_t n, uint32_t rounds, OffDesc od) {
     using R = typename RedSel<DT, OP>::R;
     using S = typename dt_traits<DT>::S;
     using V = VecT<S, VEC>;
     using St = typename R::St;
-    constexpr int U = 4;
-    const uint32_t g = blockIdx.x;     // outputs on x (up to 2^31), chunks on y (<= 2048)
+    constexpr int GPB = 256 / L;                         // groups per block
+    const uint32_t group = blockIdx.x * GPB + threadIdx.x / L;
+    const uint32_t lane = threadIdx.x % L;
+    const uint32_t ngroups = gridDim.x * GPB;
+    for (uint32_t r = 0; r < rounds; r++) {
+        St st[U];
+        const S* row[U];
+        bool valid[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            uint64_t g = (uint64_t)(r * U + u) * ngroups + group;
+            valid[u] = g < total_out;
+            row[u] = in + (valid[u] ? od.offset((uint32_t)g) : 0);
+            st[u] = R::init();
+        }
+#pragma unroll 4
+        for (uint32_t e = lane * VEC; e < n; e += L * VEC) {
+            V v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (valid[u]) v[u] = *reinterpret_cast<const V*>(row[u] + e);
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (valid[u]) {
+#pragma unroll
+                    for (int k = 0; k < VEC; k++) R::step(st[u], v[u].v[k], e + k);
+                }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int m = L / 2; m >= 1; m >>= 1) st[u] = R::combine(st[u], R::shfl(st[u], m));
+            uint64_t g = (uint64_t)(r * U + u) * ngroups + group;
+            if (valid[u] && lane == 0) out[g] = R::out(st[u]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ block (stride 1, long rows)
+// One block of 64 * WAVES threads per (output, chunk).  blockIdx.x = output, blockIdx.y = chunk.
+template <int DT, int OP, int VEC, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void reduce_block_kernel(
+    typename RedSel<DT, OP>::R::OutT* __restrict__ out, typename RedSel<DT, OP>::R::St* __restrict__ part,
+    const typename dt_traits<DT>::S* __restrict__ in, uint32_t total_out,
+    uint32_t n, uint32_t chunk, uint32_t nsplit, OffDesc od) {
+    using R = typename RedSel<DT, OP>::R;
+    using S = typename dt_traits<DT>::S;
+    using V = VecT<S, VEC>;
+    using St = typename R::St;
+    constexpr int U = 8;
+    constexpr uint32_t STEP = 64 * WAVES * VEC;
+    const uint32_t g = blockIdx.x;
     const uint32_t c = blockIdx.y;
     const uint32_t beg = c * chunk;
     const uint32_t end = min(n, beg + chunk);
     const S* row = in + od.offset(g);
     St st = R::init();
     uint32_t e = beg + threadIdx.x * VEC;
-    for (; e + (U - 1) * kBlock * VEC < end; e += U * kBlock * VEC) {
+    for (; e + (U - 1) * STEP < end; e += U * STEP) {
         V v[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const V*>(row + e + u * kBlock * VEC);
+        for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const V*>(row + e + u * STEP);
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int k = 0; k < VEC; k++) R::step(st, v[u].v[k], e + u * kBlock * VEC + k);
+            for (int k = 0; k < VEC; k++) R::step(st, v[u].v[k], e + u * STEP + k);
     }
-    for (; e < end; e += kBlock * VEC) {
+    for (; e < end; e += STEP) {
         V v = *reinterpret_cast<const V*>(row + e);
 #pragma unroll
         for (int k = 0; k < VEC; k++) R::step(st, v.v[k], e + k);
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) st = R::combine(st, R::shfl(st, m));
-    __shared__ St part[kBlock / 64];
-    const int wave = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) part[wave] = st;
+    __shared__ St wpart[WAVES];
+    if ((threadIdx.x & 63) == 0) wpart[threadIdx.x >> 6] = st;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        St r = part[0];
+    St r = wpart[0];
 #pragma unroll
-        for (int w = 1; w < kBlock / 64; w++) r = R::combine(r, part[w]);
-        if (nchunks == 1) out[g] = R::out(r);
-        else ws[(uint64_t)c * total_out + g] = r;
+    for (int w = 1; w < WAVES; w++) r = R::combine(r, wpart[w]);
+    if (threadIdx.x == 0) {
+        if (nsplit == 1) out[g] = R::out(r);
+        else part[(uint64_t)c * total_out + g] = r;
     }
 }
 
-// cols: a thread owns VEC consecutive outputs and walks the reduced axis (chunk c of it).
-template <int DT, int OP, int VEC>
-__global__ __launch_bounds__(kBlock) void reduce_cols_kernel(
-    typename RedSel<DT, OP>::R::OutT* __restrict__ out, typename RedSel<DT, OP>::R::St* __restrict__ ws,
-    const typename dt_traits<DT>::S* __restrict__ in, uint32_t total_out, uint32_t n,
-    uint32_t rs, uint32_t chunk, uint32_t nchunks, OffDesc od) {
+// ------------------------------------------------------------------ cols (stride != 1)
+// Lane l of every wave owns outputs [(blockIdx.x*64 + l)*VEC, +VEC); the WAVES waves of the block
+// take interleaved rows of the block's share [split * chunk, ...) of the reduced axis.
+template <int DT, int OP, int VEC, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void reduce_cols_kernel(
+    typename RedSel<DT, OP>::R::OutT* __restrict__ out, typename RedSel<DT, OP>::R::St* __restrict__ part,
+    const typename dt_traits<DT>::S* __restrict__ in, uint32_t total_out,
+    uint32_t n, uint32_t rs, uint32_t chunk, uint32_t nsplit, OffDesc od) {
     using R = typename RedSel<DT, OP>::R;
     using S = typename dt_traits<DT>::S;
     using V = VecT<S, VEC>;
     using St = typename R::St;
-    constexpr int U = 4;
-    const uint32_t t = blockIdx.x * kBlock + threadIdx.x;
-    const uint32_t g0 = t * VEC;
-    if (g0 >= total_out) return;
+    constexpr int U = 8;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t g0 = (blockIdx.x * 64 + lane) * VEC;
+    const bool valid = g0 < total_out;
     const uint32_t c = blockIdx.y;
     const uint32_t beg = c * chunk;
     const uint32_t end = min(n, beg + chunk);
-    const S* base = in + od.offset(g0);
+    const S* base = in + (valid ? od.offset(g0) : 0);
     St st[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; k++) st[k] = R::init();
-    uint32_t i = beg;
-    for (; i + U <= end; i += U) {
-        V v[U];
+    if (valid) {
+        uint32_t i = beg + wave;
+        for (; i + (U - 1) * WAVES < end; i += U * WAVES) {
+            V v[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)(i + u) * rs);
+            for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)(i + u * WAVES) * rs);
 #pragma unroll
-        for (int u = 0; u < U; u++)
+            for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int k = 0; k < VEC; k++) R::step(st[k], v[u].v[k], i + u);
+                for (int k = 0; k < VEC; k++) R::step(st[k], v[u].v[k], i + u * WAVES);
+        }
+        for (; i < end; i += WAVES) {
+            V v = *reinterpret_cast<const V*>(base + (uint64_t)i * rs);
+#pragma unroll
+            for (int k = 0; k < VEC; k++) R::step(st[k], v.v[k], i);
+        }
     }
-    for (; i < end; i++) {
-        V v = *reinterpret_cast<const V*>(base + (uint64_t)i * rs);
+    // combine the waves' states through LDS, in wave order
+    if constexpr (WAVES > 1) {
+        __shared__ St sh[WAVES - 1][64 * VEC];
+        if (wave > 0) {
 #pragma unroll
-        for (int k = 0; k < VEC; k++) R::step(st[k], v.v[k], i);
+            for (int k = 0; k < VEC; k++) sh[wave - 1][lane * VEC + k] = st[k];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            for (int w = 0; w < WAVES - 1; w++)
+#pragma unroll
+                for (int k = 0; k < VEC; k++) st[k] = R::combine(st[k], sh[w][lane * VEC + k]);
+        }
     }
+    if (wave == 0 && valid) {
 #pragma unroll
-    for (int k = 0; k < VEC; k++) {
-        if (nchunks == 1) out[g0 + k] = R::out(st[k]);
-        else ws[(uint64_t)c * total_out + g0 + k] = st[k];
+        for (int k = 0; k < VEC; k++) {
+            if (nsplit == 1) out[g0 + k] = R::out(st[k]);
+            else part[(uint64_t)c * total_out + g0 + k] = st[k];
+        }
     }
 }
 
-// finalize: combine chunk partials in chunk order.
+// finalize: output g combines its nsplit partials in split order.
 template <int DT, int OP>
-__global__ __launch_bounds__(kBlock) void reduce_finalize_kernel(
-    typename RedSel<DT, OP>::R::OutT* __restrict__ out, const typename RedSel<DT, OP>::R::St* __restrict__ ws,
-    uint32_t total_out, uint32_t nchunks) {
+__global__ __launch_bounds__(256) void reduce_finalize_kernel(
+    typename RedSel<DT, OP>::R::OutT* __restrict__ out, const typename RedSel<DT, OP>::R::St* __restrict__ part,
+    uint32_t total_out, uint32_t nsplit) {
     using R = typename RedSel<DT, OP>::R;
-    const uint32_t g = blockIdx.x * kBlock + threadIdx.x;
+    const uint32_t g = blockIdx.x * 256 + threadIdx.x;
     if (g >= total_out) return;
-    typename R::St r = ws[g];
-    for (uint32_t c = 1; c < nchunks; c++) r = R::combine(r, ws[(uint64_t)c * total_out + g]);
-    out[g] = R::out(r);
+    typename R::St a = part[g];
+    for (uint32_t s = 1; s < nsplit; s++) a = R::combine(a, part[(uint64_t)s * total_out + g]);
+    out[g] = R::out(a);
+}
+
+// finalize for many partials per output: one 256-thread block per output, a fixed-shape tree.
+template <int DT, int OP>
+__global__ __launch_bounds__(256) void reduce_finalize_wide_kernel(
+    typename RedSel<DT, OP>::R::OutT* __restrict__ out, const typename RedSel<DT, OP>::R::St* __restrict__ part,
+    uint32_t total_out, uint32_t nsplit) {
+    using R = typename RedSel<DT, OP>::R;
+    using St = typename R::St;
+    const uint32_t g = blockIdx.x;
+    St a = R::init();
+    for (uint32_t s = threadIdx.x; s < nsplit; s += 256) a = R::combine(a, part[(uint64_t)s * total_out + g]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) a = R::combine(a, R::shfl(a, m));
+    __shared__ St w[4];
+    if ((threadIdx.x & 63) == 0) w[threadIdx.x >> 6] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) out[g] = R::out(R::combine(R::combine(w[0], w[1]), R::combine(w[2], w[3])));
 }
 
 // ------------------------------------------------------------------ planning
 enum Mode { kRows = 0, kBlockMode = 1, kCols = 2 };
-
-struct Plan {
-    Mode mode = kCols;
-    int vec = 1;
-    int lanes = 1;
-    uint32_t nchunks = 1;
-    uint32_t chunk = 0;
-    uint32_t total_out = 0;
-    size_t state_bytes = 0;
-    size_t ws_bytes() const { return nchunks > 1 ? (size_t)nchunks * total_out * state_bytes : 0; }
-};
-
-template <int DT, int OP>
-size_t state_size() { return sizeof(typename RedSel<DT, OP>::R::St); }
 
 struct Desc {
     int cd;
@@ -296,7 +354,25 @@ struct Desc {
     uint32_t rs, n;
 };
 
-// The chunking depends only on the descriptor (never on pointer alignment), so the
+struct Plan {
+    Mode mode = kCols;
+    int vec = 1;            // elements per 128-bit load actually used (1 = scalar loads)
+    int lanes = 1;          // rows plan: lanes per output
+    int unroll = 1;         // rows plan: outputs in flight per lane group
+    int waves = 1;          // cols plan: waves per block
+    uint32_t blocks = 0;    // rows plan: grid size; cols plan: column groups
+    uint32_t rounds = 0;
+    uint32_t nsplit = 1;    // blocks sharing one output's axis
+    uint32_t chunk = 0;     // axis elements per split
+    uint32_t total_out = 0;
+    size_t state_bytes = 0;
+    size_t ws_bytes() const { return nsplit > 1 ? (size_t)nsplit * total_out * state_bytes : 0; }
+};
+
+constexpr uint32_t kTargetBlocks = 2048;     // 8 resident 256-thread blocks per CU on 256 CUs
+constexpr uint64_t kColsLdsBytes = 32768;    // LDS budget of the cols plan's cross-wave combine
+
+// The split layout depends only on the descriptor (never on pointer alignment), so the
 // workspace size reported ahead of time always covers the launch.
 Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
     Plan p;
@@ -306,6 +382,7 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
     p.state_bytes = stbytes;
     const int VEC = (int)(16 / elem);
     const bool aligned = in_ptr % 16 == 0;
+    if (tot == 0) return p;
     if (d.rs == 1 && d.n > 1) {
         bool v_ok = VEC > 1 && d.n % VEC == 0;
         for (int i = 0; v_ok && i < d.cd; i++) if (d.si[i] % VEC) v_ok = false;
@@ -313,18 +390,30 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
         p.vec = (v_ok && aligned) ? VEC : 1;
         const uint32_t nv = (d.n + nominal - 1) / nominal;
         if (nv > 1024) {
+            // One block per output when there are enough outputs to cover the CUs (no partials,
+            // no cross-block step); otherwise split each row into chunks of >= 4 vectors a thread.
             p.mode = kBlockMode;
-            const uint32_t per_block = 2048;      // vectors per block (8 per thread)
-            uint64_t want = (2048 + tot - 1) / tot;
-            uint64_t maxc = (nv + per_block - 1) / per_block;
+            p.waves = nv >= 8192 ? 16 : 4;
+            const uint64_t threads = 64ull * p.waves;
+            const uint64_t want_blocks = p.waves == 16 ? 256 : 1024;
+            uint64_t want = (want_blocks + tot - 1) / tot;
+            uint64_t maxc = (nv + threads * 4 - 1) / (threads * 4);
             uint64_t nc = want < maxc ? want : maxc;
             if (nc < 1) nc = 1;
             uint32_t chunk_v = (uint32_t)((nv + nc - 1) / nc);
             p.chunk = chunk_v * nominal;
-            p.nchunks = (d.n + p.chunk - 1) / p.chunk;
+            p.nsplit = (d.n + p.chunk - 1) / p.chunk;
         } else {
             p.mode = kRows;
             p.lanes = nv <= 2 ? 1 : nv <= 16 ? 4 : nv <= 64 ? 16 : 64;
+            p.unroll = p.lanes == 64 ? 1 : 4;
+            const uint64_t groups_needed = (tot + p.unroll - 1) / p.unroll;
+            const uint64_t gpb = 256 / p.lanes;
+            uint64_t blocks = (groups_needed + gpb - 1) / gpb;
+            if (blocks > 8 * kTargetBlocks) blocks = 8 * kTargetBlocks;
+            p.blocks = (uint32_t)blocks;
+            const uint64_t per_round = blocks * gpb * p.unroll;
+            p.rounds = (uint32_t)((tot + per_round - 1) / per_round);
         }
         return p;
     }
@@ -333,23 +422,32 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
     bool v_ok = VEC > 1 && d.so[last] == 1 && d.si[last] == 1 && d.shape[last] % VEC == 0 &&
                 d.rs % VEC == 0;
     for (int i = 0; v_ok && i < last; i++) if (d.si[i] % VEC || d.so[i] % VEC) v_ok = false;
+    const uint32_t nominal = v_ok ? (uint32_t)VEC : 1u;
     p.mode = kCols;
     p.vec = (v_ok && aligned) ? VEC : 1;
-    const uint64_t threads = tot / (v_ok ? VEC : 1);
-    p.nchunks = 1;
-    if (d.n >= 64 && threads < 131072) {
-        uint64_t want = (131072 + threads - 1) / threads;
-        uint64_t maxc = d.n / 16;
-        if (maxc > 4096) maxc = 4096;          // grid.y stays far below its 65535 limit
+    p.waves = d.n >= 64 ? 16 : (d.n >= 16 ? 4 : 1);
+    if (p.waves == 16 && 15ull * 64 * nominal * stbytes > kColsLdsBytes) p.waves = 4;
+    const uint64_t groups = (tot + 64ull * nominal - 1) / (64ull * nominal);   // blocks along x
+    p.blocks = (uint32_t)groups;
+    // split the axis over blocks when the grid would leave CUs idle
+    const uint64_t waves_total = groups * p.waves;
+    p.nsplit = 1;
+    if (waves_total < 4096 && d.n >= 256) {
+        uint64_t want = (4096 + waves_total - 1) / waves_total;
+        uint64_t maxc = d.n / 128;                 // keep >= 128 axis elements per split
+        if (maxc > 4096) maxc = 4096;
         uint64_t nc = want < maxc ? want : maxc;
         if (nc > 1) {
             p.chunk = (uint32_t)((d.n + nc - 1) / nc);
-            p.nchunks = (d.n + p.chunk - 1) / p.chunk;
+            p.nsplit = (d.n + p.chunk - 1) / p.chunk;
         }
     }
-    if (p.nchunks == 1) p.chunk = d.n;
+    if (p.nsplit == 1) p.chunk = d.n;
     return p;
 }
+
+template <int DT, int OP>
+size_t state_size() { return sizeof(typename RedSel<DT, OP>::R::St); }
 
 template <int DT, int OP>
 int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -368,37 +466,55 @@ int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, h
     for (int i = 0; i < d.cd; i++) { od.so[i] = FastDiv(d.so[i]); od.si[i] = d.si[i]; }
     OutT* out = (OutT*)outp;
     const S* in = (const S*)inp;
-    StT* wsp = (StT*)ws;
+    StT* part = (StT*)ws;
+    const bool vec = p.vec == VEC && VEC > 1;
     if (p.mode == kRows) {
-        uint64_t threads = (uint64_t)p.total_out * p.lanes;
-        dim3 grid((uint32_t)((threads + kBlock - 1) / kBlock));
-#define MX_ROWS(V_, L_) hipLaunchKernelGGL((reduce_rows_kernel<DT, OP, V_, L_>), grid, dim3(kBlock), 0, st, out, in, p.total_out, d.n, od)
-        if (p.vec == VEC && VEC > 1) {
-            switch (p.lanes) { case 1: MX_ROWS(VEC, 1); break; case 4: MX_ROWS(VEC, 4); break;
-                               case 16: MX_ROWS(VEC, 16); break; default: MX_ROWS(VEC, 64); break; }
+        dim3 grid(p.blocks);
+#define MX_ROWS(V_, L_, U_) hipLaunchKernelGGL((reduce_rows_kernel<DT, OP, V_, L_, U_>), grid, dim3(256), 0, st, \
+                                               out, in, p.total_out, d.n, p.rounds, od)
+        if (vec) {
+            switch (p.lanes) { case 1: MX_ROWS(VEC, 1, 4); break; case 4: MX_ROWS(VEC, 4, 4); break;
+                               case 16: MX_ROWS(VEC, 16, 4); break; default: MX_ROWS(VEC, 64, 1); break; }
         } else {
-            switch (p.lanes) { case 1: MX_ROWS(1, 1); break; case 4: MX_ROWS(1, 4); break;
-                               case 16: MX_ROWS(1, 16); break; default: MX_ROWS(1, 64); break; }
+            switch (p.lanes) { case 1: MX_ROWS(1, 1, 4); break; case 4: MX_ROWS(1, 4, 4); break;
+                               case 16: MX_ROWS(1, 16, 4); break; default: MX_ROWS(1, 64, 1); break; }
         }
 #undef MX_ROWS
     } else if (p.mode == kBlockMode) {
-        dim3 grid(p.total_out, p.nchunks);
-        if (p.vec == VEC && VEC > 1)
-            hipLaunchKernelGGL((reduce_block_kernel<DT, OP, VEC>), grid, dim3(kBlock), 0, st, out, wsp, in, p.total_out, d.n, p.chunk, p.nchunks, od);
-        else
-            hipLaunchKernelGGL((reduce_block_kernel<DT, OP, 1>), grid, dim3(kBlock), 0, st, out, wsp, in, p.total_out, d.n, p.chunk, p.nchunks, od);
+        dim3 grid(p.total_out, p.nsplit);
+#define MX_BLOCK(V_, W_) hipLaunchKernelGGL((reduce_block_kernel<DT, OP, V_, W_>), grid, dim3(64 * W_), 0, st, \
+                                            out, part, in, p.total_out, d.n, p.chunk, p.nsplit, od)
+        if (vec) {
+            if (p.waves == 16) MX_BLOCK(VEC, 16); else MX_BLOCK(VEC, 4);
+        } else {
+            if (p.waves == 16) MX_BLOCK(1, 16); else MX_BLOCK(1, 4);
+        }
+#undef MX_BLOCK
     } else {
-        uint32_t threads = p.total_out / p.vec;
-        dim3 grid((threads + kBlock - 1) / kBlock, p.nchunks);
-        if (p.vec == VEC && VEC > 1)
-            hipLaunchKernelGGL((reduce_cols_kernel<DT, OP, VEC>), grid, dim3(kBlock), 0, st, out, wsp, in, p.total_out, d.n, d.rs, p.chunk, p.nchunks, od);
-        else
-            hipLaunchKernelGGL((reduce_cols_kernel<DT, OP, 1>), grid, dim3(kBlock), 0, st, out, wsp, in, p.total_out, d.n, d.rs, p.chunk, p.nchunks, od);
+        // the x extent is in units of 64 lanes x the vector width actually used
+        const uint32_t gx = (uint32_t)((p.total_out + 64ull * p.vec - 1) / (64ull * p.vec));
+        dim3 grid(gx, p.nsplit);
+#define MX_COLS(V_, W_) hipLaunchKernelGGL((reduce_cols_kernel<DT, OP, V_, W_>), grid, dim3(64 * W_), 0, st, \
+                                           out, part, in, p.total_out, d.n, d.rs, p.chunk, p.nsplit, od)
+        if (vec) {
+            if constexpr (15ull * 64 * VEC * sizeof(StT) <= kColsLdsBytes) {
+                switch (p.waves) { case 16: MX_COLS(VEC, 16); break; case 4: MX_COLS(VEC, 4); break; default: MX_COLS(VEC, 1); break; }
+            } else {
+                switch (p.waves) { case 4: MX_COLS(VEC, 4); break; default: MX_COLS(VEC, 1); break; }
+            }
+        } else {
+            switch (p.waves) { case 16: MX_COLS(1, 16); break; case 4: MX_COLS(1, 4); break; default: MX_COLS(1, 1); break; }
+        }
+#undef MX_COLS
     }
     MX_HIP(hipGetLastError());
-    if (p.nchunks > 1) {
-        dim3 grid((p.total_out + kBlock - 1) / kBlock);
-        hipLaunchKernelGGL((reduce_finalize_kernel<DT, OP>), grid, dim3(kBlock), 0, st, out, wsp, p.total_out, p.nchunks);
+    if (p.nsplit > 32 && p.total_out <= 65535u * 16) {
+        hipLaunchKernelGGL((reduce_finalize_wide_kernel<DT, OP>), dim3(p.total_out), dim3(256), 0, st, out, part,
+                           p.total_out, p.nsplit);
+        MX_HIP(hipGetLastError());
+    } else if (p.nsplit > 1) {
+        dim3 grid((p.total_out + 255) / 256);
+        hipLaunchKernelGGL((reduce_finalize_kernel<DT, OP>), grid, dim3(256), 0, st, out, part, p.total_out, p.nsplit);
         MX_HIP(hipGetLastError());
     }
     return MX_OK;
@@ -460,8 +576,6 @@ extern "C" int mx_reduce_workspace_bytes(int op, int dtype, uint32_t reduce_stri
         dispatch_op(op, [&](auto o) { st = state_size<DT, decltype(o)::value>(); });
     });
     if (!ok) return fail(MX_ERR_UNSUPPORTED, "mx_reduce_workspace_bytes: no kernel for dtype " + std::to_string(dtype));
-    // Alignment only changes the vector width, never the chunking of the column plan; the
-    // row plan's chunking depends on it, so size for the worst case (aligned input).
     Plan p = make_plan(d, el, st, 0);
     *bytes = p.ws_bytes();
     return MX_OK;

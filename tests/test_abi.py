@@ -69,8 +69,10 @@ def test_unsupported_dtype_and_uninitialized_runtime():
 
 
 def test_workspace_query_is_pure_host():
-    # the row-sum plan of [256, 65536] splits each row over several blocks -> needs partials
-    nb = mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 65536, ([256], [1], [65536]))
-    assert nb > 0 and nb % (256 * 4) == 0
+    # 4 rows of 2^20 are too few outputs for the CUs: each row is split -> partials + counters
+    nb = mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 1 << 20, ([4], [1], [1 << 20]))
+    assert nb > 0
+    # 256 rows of 65536 take one block per row: no workspace
+    assert mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 65536, ([256], [1], [65536])) == 0
     # add+row-sum's [4096, 1024] needs none
     assert mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 1024, ([4096], [1], [1024])) == 0

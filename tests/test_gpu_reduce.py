@@ -34,9 +34,18 @@ def run_reduce(mx, orc, op, code, x_flat, shape, axis, in_strides=None, keepdims
     O = mx.DeviceBuffer(max(total, 1) * np.dtype(out_dt).itemsize)
     wsb = mx.reduce_workspace_bytes(op, code, rs, n, desc)
     W = mx.DeviceBuffer(wsb) if wsb else None
+    if W:
+        W.fill_bytes(0)
     mx.launch_reduce(op, code, rs, n, desc, O.ptr, X.ptr, W.ptr if W else 0, wsb)
     mx.sync()
     got = O.download(out_dt, total)
+    if W:
+        # the split plan leaves its arrival counters at zero: a second launch on the same
+        # workspace gives the same bits
+        O2 = mx.DeviceBuffer(max(total, 1) * np.dtype(out_dt).itemsize)
+        mx.launch_reduce(op, code, rs, n, desc, O2.ptr, X.ptr, W.ptr, wsb)
+        mx.sync()
+        assert np.array_equal(bits(O2.download(out_dt, total)), bits(got))
     ref = orc.reduce(op, code, rs, n, desc, total, x_flat, acc=orc.ACC_F32 if acc is None else acc)
     return got, ref, desc, rs, n
 
@@ -119,7 +128,8 @@ def test_add_rowsum_sum(mx, orc):
 
 @pytest.mark.parametrize("shape,axis", [([3, 5], 1), ([7, 2], 1), ([9, 40], 1), ([11, 200], 1), ([5, 3000], 1),
                                         ([2, 50000], 1), ([37, 53], 0), ([4, 5, 6, 7], 2), ([4, 5, 6, 7], 0),
-                                        ([1, 1], 0), ([6, 1, 8], 1), ([3, 4, 5], 2)])
+                                        ([1, 1], 0), ([6, 1, 8], 1), ([3, 4, 5], 2), ([3000, 8], 0),
+                                        ([20000, 12], 0), ([700, 36], 0), ([5, 100003], 1), ([129, 1000], 0)])
 @pytest.mark.parametrize("opn", OPS)
 def test_plans_f32(mx, orc, shape, axis, opn):
     """Covers every plan: L-lane rows, block + finalize, columns with and without chunks."""
@@ -224,10 +234,24 @@ def test_empty_reduced_axis(mx, orc):
 
 
 def test_workspace_too_small_is_an_error(mx):
-    desc = [[256], [1], [65536]]
-    nb = mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 65536, desc)
+    # 4 rows of 2^20: too few outputs to cover the CUs, so each row is split over blocks
+    desc = [[4], [1], [1 << 20]]
+    nb = mx.reduce_workspace_bytes(mx.RED_SUM, mx.FLOAT32, 1, 1 << 20, desc)
     assert nb > 0
-    X = mx.DeviceBuffer(256 * 65536 * 4)
-    O = mx.DeviceBuffer(256 * 4)
+    X = mx.DeviceBuffer(4 * (1 << 20) * 4)
+    O = mx.DeviceBuffer(4 * 4)
     with pytest.raises(mx.MatrixAMDError, match="workspace"):
-        mx.launch_reduce(mx.RED_SUM, mx.FLOAT32, 1, 65536, desc, O.ptr, X.ptr, 0, 0)
+        mx.launch_reduce(mx.RED_SUM, mx.FLOAT32, 1, 1 << 20, desc, O.ptr, X.ptr, 0, 0)
+
+
+@pytest.mark.parametrize("opn", OPS)
+def test_split_rows_few_outputs(mx, orc, opn):
+    """Few long rows: the axis is split over blocks and the last block combines."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(6)
+    x = np.round(rng.standard_normal([3, 1 << 20]) * 4).astype(np.float32)
+    got, ref, *_ = run_reduce(mx, orc, op, mx.FLOAT32, x.ravel(), [3, 1 << 20], 1)
+    if op == mx.RED_SUM:
+        check_sum(got, ref, np.abs(x.astype(np.float64)).sum(1))
+    else:
+        assert np.array_equal(bits(got), bits(ref))
