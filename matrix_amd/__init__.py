@@ -290,6 +290,13 @@ def reduce_workspace_bytes(op, dtype, reduce_stride, n_reduce, desc):
     return nb.value
 
 
+def launch_batched_matmul(dtype, desc, K, C, A, Bt, stream=None):
+    """desc = (shapeC [..., M, N], sA, sBt, sC) as collapse_dims_matmul gives it."""
+    shape, sA, sBt, sC = desc
+    check(lib.mx_launch_batched_matmul(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
+                                       int(C), int(A), int(Bt), stream))
+
+
 def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=0, workspace_bytes=0,
                   stream=None):
     shape, sOut, sIn = desc

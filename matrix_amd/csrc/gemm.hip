@@ -1,0 +1,415 @@
+// gemm.hip -- batched C[b, m, n] = sum_k A[b, m, k] * Bt[b, n, k] on CDNA4 matrix cores.
+//
+// Replaces dot_gpu / batched_dot_gpu (Matrix.mm:7198-7291), whose Metal kernel computes one
+// output per thread (MatMul.metal:46-102).  The reference always hands the backend A [..., M, K]
+// and Bt [..., N, K] with K innermost (dot() packs B^T, Matrix.mm:7074-7089), i.e. both operands
+// K-major -- the layout MFMA wants.
+//
+// float16 / bfloat16: v_mfma_f32_32x32x16_{f16,bf16}, fp32 accumulation, one rounding on store.
+// float32:            v_mfma_f32_32x32x2_f32, fp32 accumulation.
+// Other dtypes:       a scalar kernel accumulating in the element type (wrap-around), as the
+//                     reference's `T sum` loop does (Matrix.mm:7187-7191).
+//
+// Tiling (MFMA path): a 256-thread block computes a 256 x 256 tile of C as 2 x 2 waves of
+// 128 x 128 (4 x 4 MFMA tiles of 32 x 32, 256 fp32 accumulators per lane).  Each K step stages
+// 256 rows x 128 bytes of A and of Bt in LDS (64 elements of 16-bit data, 32 of fp32), double
+// buffered: the next step's global loads are in flight while the current step's MFMAs run.
+// LDS rows are 8 chunks of 16 bytes; chunk c of row r lives at c ^ (r & 7) so that the 32 rows
+// one MFMA operand read touches spread over all banks.
+// Block ids are remapped so that the tiles one XCD (one L2) runs are consecutive M panels with
+// all their N tiles: each A panel is fetched into an L2 once and reused across N.
+// When Bt is shared by the whole batch (batch stride 0) and A / C stack their batches
+// contiguously, the batch folds into M.
+#include "common.hpp"
+
+namespace mx {
+namespace {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef __bf16 b8v __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 256;
+constexpr int ROWB = 128;                 // bytes of one LDS tile row per K step
+constexpr int NTHREADS = 256;
+constexpr int STAGE_BYTES = BM * ROWB;    // one operand, one stage: 32 KB
+constexpr int NUM_XCD = 8;
+
+template <int DT> struct MmaTraits;
+template <> struct MmaTraits<MX_FLOAT16> { using S = uint16_t; };
+template <> struct MmaTraits<MX_BFLOAT16> { using S = uint16_t; };
+template <> struct MmaTraits<MX_FLOAT32> { using S = float; };
+
+struct BatchDesc {                // batch axes of the collapsed descriptor (all but the last two)
+    int n;
+    FastDiv shape[MX_MAX_DIMS];
+    uint32_t sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sC[MX_MAX_DIMS];
+};
+
+struct GemmArgs {
+    uint32_t M, N, K;
+    uint32_t lda, ldb;            // row strides (elements) of A [M, K] and Bt [N, K]
+    uint32_t ka, kb;              // K strides of A and Bt (1 on the vector path)
+    uint32_t ldc, cn;             // C strides: row (M) and column (N)
+    uint32_t tiles_m, tiles_n, batches;
+    BatchDesc bd;
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+
+// Block id -> (batch, tile_m, tile_n).  Hardware dispatch hands block i to XCD i % 8; the
+// remap gives each XCD a contiguous run of logical tiles, ordered M panel by M panel.
+__device__ __forceinline__ void tile_of(uint32_t id, uint32_t nblocks, uint32_t tiles_m, uint32_t tiles_n,
+                                        uint32_t& b, uint32_t& tm, uint32_t& tn) {
+    const uint32_t per = nblocks / NUM_XCD, rem = nblocks % NUM_XCD;
+    const uint32_t x = id % NUM_XCD, j = id / NUM_XCD;
+    const uint32_t logical = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const uint32_t tiles = tiles_m * tiles_n;
+    b = logical / tiles;
+    const uint32_t t = logical - b * tiles;
+    tm = t / tiles_n;
+    tn = t - tm * tiles_n;
+}
+
+// Loads this thread's 8 chunks (16 B each) of a 256-row operand tile at K offset k0 into regs.
+// Chunk q = tid + 256 i covers row q / 8, bytes (q % 8) * 16 of that row's 128-byte K slice.
+template <typename S, bool VEC>
+__device__ __forceinline__ void load_tile(uint4 (&r)[8], const S* __restrict__ base, uint32_t rows_valid,
+                                          uint32_t ld, uint32_t kstride, uint32_t k0, uint32_t K) {
+    constexpr int CE = 16 / sizeof(S);    // elements per chunk
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int q = threadIdx.x + NTHREADS * i;
+        const int row = q >> 3, c = q & 7;
+        const uint32_t k = k0 + c * CE;
+        if (VEC && row < (int)rows_valid && k + CE <= K) {
+            r[i] = *reinterpret_cast<const uint4*>(base + (uint64_t)row * ld + k);
+        } else {
+            S tmp[CE];
+#pragma unroll
+            for (int e = 0; e < CE; e++) {
+                const bool ok = row < (int)rows_valid && k + e < K;
+                tmp[e] = ok ? base[(uint64_t)row * ld + (uint64_t)(k + e) * kstride] : S(0);
+            }
+            __builtin_memcpy(&r[i], tmp, 16);
+        }
+    }
+}
+
+__device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int q = threadIdx.x + NTHREADS * i;
+        const int row = q >> 3, c = q & 7;
+        *reinterpret_cast<uint4*>(lds + row * ROWB + swz(row, c) * 16) = r[i];
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void mma_kblock(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
+                                           int wm, int wn, int lane);
+
+// 16-bit: one K block = 16 elements = 2 chunks; lane half h reads chunk 2 kb + h (8 elements).
+template <>
+__device__ __forceinline__ void mma_kblock<MX_FLOAT16>(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
+                                                       int wm, int wn, int lane) {
+    const int r32 = lane & 31, h = lane >> 5;
+    h8v a[4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int ra = wm * 128 + t * 32 + r32;
+        const int rb = wn * 128 + t * 32 + r32;
+        a[t] = *reinterpret_cast<const h8v*>(la + ra * ROWB + swz(ra, 2 * kb + h) * 16);
+        b[t] = *reinterpret_cast<const h8v*>(lb + rb * ROWB + swz(rb, 2 * kb + h) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+template <>
+__device__ __forceinline__ void mma_kblock<MX_BFLOAT16>(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
+                                                        int wm, int wn, int lane) {
+    const int r32 = lane & 31, h = lane >> 5;
+    b8v a[4], b[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int ra = wm * 128 + t * 32 + r32;
+        const int rb = wn * 128 + t * 32 + r32;
+        a[t] = *reinterpret_cast<const b8v*>(la + ra * ROWB + swz(ra, 2 * kb + h) * 16);
+        b[t] = *reinterpret_cast<const b8v*>(lb + rb * ROWB + swz(rb, 2 * kb + h) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+}
+
+// fp32: one K block = 16 elements = 4 chunks; lane half h holds K offsets 8h..8h+7 (2 chunks)
+// and the 8 MFMA substeps s each consume element s: the two lane halves supply k = s and 8 + s.
+template <>
+__device__ __forceinline__ void mma_kblock<MX_FLOAT32>(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
+                                                       int wm, int wn, int lane) {
+    const int r32 = lane & 31, h = lane >> 5;
+    float a[4][8], b[4][8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int ra = wm * 128 + t * 32 + r32;
+        const int rb = wn * 128 + t * 32 + r32;
+        const float4 a0 = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 4 * kb + 2 * h) * 16);
+        const float4 a1 = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 4 * kb + 2 * h + 1) * 16);
+        const float4 b0 = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 4 * kb + 2 * h) * 16);
+        const float4 b1 = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 4 * kb + 2 * h + 1) * 16);
+        a[t][0] = a0.x; a[t][1] = a0.y; a[t][2] = a0.z; a[t][3] = a0.w;
+        a[t][4] = a1.x; a[t][5] = a1.y; a[t][6] = a1.z; a[t][7] = a1.w;
+        b[t][0] = b0.x; b[t][1] = b0.y; b[t][2] = b0.z; b[t][3] = b0.w;
+        b[t][4] = b1.x; b[t][5] = b1.y; b[t][6] = b1.z; b[t][7] = b1.w;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<DT>::S* __restrict__ C,
+                                                             const typename MmaTraits<DT>::S* __restrict__ A,
+                                                             const typename MmaTraits<DT>::S* __restrict__ Bt,
+                                                             GemmArgs g) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr int KSTEP = ROWB / sizeof(S);            // elements of K per LDS stage
+    constexpr int KBLOCKS = KSTEP / 16;
+    extern __shared__ __align__(16) char smem[];
+    // stage s of A at smem + s * STAGE_BYTES, of Bt at smem + (2 + s) * STAGE_BYTES
+    auto lds_a = [&](int s) { return smem + s * STAGE_BYTES; };
+    auto lds_b = [&](int s) { return smem + (2 + s) * STAGE_BYTES; };
+
+    uint32_t bidx, tm, tn;
+    tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, bidx, tm, tn);
+    // batch offsets
+    uint64_t offA = 0, offB = 0, offC = 0;
+    {
+        uint32_t rem = bidx;
+        for (int d = g.bd.n - 1; d >= 0; --d) {
+            uint32_t q = g.bd.shape[d].div(rem);
+            uint32_t idx = rem - q * g.bd.shape[d].d;
+            rem = q;
+            offA += (uint64_t)idx * g.bd.sA[d];
+            offB += (uint64_t)idx * g.bd.sB[d];
+            offC += (uint64_t)idx * g.bd.sC[d];
+        }
+    }
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const S* Ablk = A + offA + (uint64_t)m0 * g.lda;
+    const S* Bblk = Bt + offB + (uint64_t)n0 * g.ldb;
+    const uint32_t rows_a = g.M - m0 < (uint32_t)BM ? g.M - m0 : (uint32_t)BM;
+    const uint32_t rows_b = g.N - n0 < (uint32_t)BN ? g.N - n0 : (uint32_t)BN;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    f16v acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const uint32_t KT = (g.K + KSTEP - 1) / KSTEP;
+    uint4 ra[8], rb[8];
+    load_tile<S, VEC>(ra, Ablk, rows_a, g.lda, g.ka, 0, g.K);
+    load_tile<S, VEC>(rb, Bblk, rows_b, g.ldb, g.kb, 0, g.K);
+    store_tile(lds_a(0), ra);
+    store_tile(lds_b(0), rb);
+    __syncthreads();
+    for (uint32_t kt = 0; kt < KT; kt++) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < KT;
+        if (more) {
+            load_tile<S, VEC>(ra, Ablk, rows_a, g.lda, g.ka, (kt + 1) * KSTEP, g.K);
+            load_tile<S, VEC>(rb, Bblk, rows_b, g.ldb, g.kb, (kt + 1) * KSTEP, g.K);
+        }
+#pragma unroll
+        for (int kb = 0; kb < KBLOCKS; kb++) mma_kblock<DT>(acc, lds_a(cur), lds_b(cur), kb, wm, wn, lane);
+        if (more) {
+            store_tile(lds_a(cur ^ 1), ra);
+            store_tile(lds_b(cur ^ 1), rb);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: acc[i][j][r] is C[row, col] with row = 32 i + 8 (r / 4) + 4 h + r % 4, col = 32 j + lane % 32
+    S* Cblk = C + offC;
+    const int h = lane >> 5, c32 = lane & 31;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t col = n0 + wn * 128 + j * 32 + c32;
+            if (col >= g.N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                if (row < g.M) {
+                    const float v = acc[i][j][r];
+                    S o;
+                    if constexpr (DT == MX_FLOAT32) o = v;
+                    else if constexpr (DT == MX_FLOAT16) o = float_to_half_bits(v);
+                    else o = float_to_bf16(v);
+                    Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = o;
+                }
+            }
+        }
+}
+
+// Scalar kernel for integer (and bool) dtypes: one output per thread, K loop in the element
+// type with wrap-around, any strides.
+template <int DT>
+__global__ __launch_bounds__(256) void gemm_scalar_kernel(typename dt_traits<DT>::S* __restrict__ C,
+                                                          const typename dt_traits<DT>::S* __restrict__ A,
+                                                          const typename dt_traits<DT>::S* __restrict__ Bt,
+                                                          GemmArgs g) {
+    using S = typename dt_traits<DT>::S;
+    using U = std::conditional_t<(sizeof(S) <= 4), uint32_t, uint64_t>;
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t per_batch = (uint64_t)g.M * g.N;
+    if (t >= per_batch * g.batches) return;
+    uint32_t bidx = (uint32_t)(t / per_batch);
+    const uint64_t mn = t - (uint64_t)bidx * per_batch;
+    const uint32_t m = (uint32_t)(mn / g.N), n = (uint32_t)(mn - (uint64_t)m * g.N);
+    uint64_t offA = 0, offB = 0, offC = 0;
+    for (int d = g.bd.n - 1; d >= 0; --d) {
+        uint32_t q = g.bd.shape[d].div(bidx);
+        uint32_t idx = bidx - q * g.bd.shape[d].d;
+        bidx = q;
+        offA += (uint64_t)idx * g.bd.sA[d];
+        offB += (uint64_t)idx * g.bd.sB[d];
+        offC += (uint64_t)idx * g.bd.sC[d];
+    }
+    const S* a = A + offA + (uint64_t)m * g.lda;
+    const S* b = Bt + offB + (uint64_t)n * g.ldb;
+    if constexpr (DT == MX_BOOL) {
+        int acc = 0;               // bool: sum += a * b stored as (sum != 0)
+        for (uint32_t k = 0; k < g.K; k++) acc = ((acc + a[(uint64_t)k * g.ka] * b[(uint64_t)k * g.kb]) != 0);
+        C[offC + (uint64_t)m * g.ldc + (uint64_t)n * g.cn] = (S)acc;
+    } else {
+        U acc = 0;
+        for (uint32_t k = 0; k < g.K; k++) acc += (U)a[(uint64_t)k * g.ka] * (U)b[(uint64_t)k * g.kb];
+        C[offC + (uint64_t)m * g.ldc + (uint64_t)n * g.cn] = (S)acc;
+    }
+}
+
+template <int DT>
+int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr int CE = 16 / sizeof(S);
+    const bool vec = g.ka == 1 && g.kb == 1 && g.lda % CE == 0 && g.ldb % CE == 0 &&
+                     (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0 && [&] {
+                         for (int d = 0; d < g.bd.n; d++)
+                             if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
+                         return true;
+                     }();
+    g.tiles_m = (g.M + BM - 1) / BM;
+    g.tiles_n = (g.N + BN - 1) / BN;
+    const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches;
+    if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: grid too large");
+    const size_t lds = 4 * STAGE_BYTES;
+    if (vec) {
+        static bool attr_set = false;
+        if (!attr_set) {
+            MX_HIP(hipFuncSetAttribute((const void*)gemm_mfma_kernel<DT, true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            attr_set = true;
+        }
+        hipLaunchKernelGGL((gemm_mfma_kernel<DT, true>), dim3((uint32_t)blocks), dim3(NTHREADS), lds, st,
+                           (S*)C, (const S*)A, (const S*)Bt, g);
+    } else {
+        static bool attr_set = false;
+        if (!attr_set) {
+            MX_HIP(hipFuncSetAttribute((const void*)gemm_mfma_kernel<DT, false>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            attr_set = true;
+        }
+        hipLaunchKernelGGL((gemm_mfma_kernel<DT, false>), dim3((uint32_t)blocks), dim3(NTHREADS), lds, st,
+                           (S*)C, (const S*)A, (const S*)Bt, g);
+    }
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
+template <int DT>
+int launch_scalar(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
+    using S = typename dt_traits<DT>::S;
+    const uint64_t total = (uint64_t)g.M * g.N * g.batches;
+    const uint64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: grid too large");
+    hipLaunchKernelGGL((gemm_scalar_kernel<DT>), dim3((uint32_t)blocks), dim3(256), 0, st, (S*)C, (const S*)A,
+                       (const S*)Bt, g);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                        const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
+                                        const void* A, const void* Bt, void* stream) {
+    if (cdims < 2 || cdims > MX_MAX_DIMS)
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: cdims " + std::to_string(cdims) + " outside [2, 8]");
+    if (!shapeC || !sA || !sBt || !sC) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: null descriptor");
+    GemmArgs g{};
+    g.M = shapeC[cdims - 2];
+    g.N = shapeC[cdims - 1];
+    g.K = K;
+    g.lda = sA[cdims - 2];
+    g.ka = sA[cdims - 1];
+    g.ldb = sBt[cdims - 2];
+    g.kb = sBt[cdims - 1];
+    g.ldc = sC[cdims - 2];
+    g.cn = sC[cdims - 1];
+    uint64_t batches = 1;
+    for (int d = 0; d < cdims - 2; d++) batches *= shapeC[d];
+    if (batches == 0 || g.M == 0 || g.N == 0) return MX_OK;
+    if (batches * g.M > 0xffffffffull || batches * g.N > 0xffffffffull)
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: extent above 2^32-1 (size_m indexing)");
+    if (!C || ((!A || !Bt) && K > 0)) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: null buffer");
+    // Fold the batch into M when Bt is shared by every batch and A and C stack their batches as
+    // consecutive row blocks (one batch axis, A stride M*lda, C stride M*ldc).
+    g.bd.n = cdims - 2;
+    for (int d = 0; d < cdims - 2; d++) {
+        g.bd.shape[d] = FastDiv(shapeC[d]);
+        g.bd.sA[d] = sA[d]; g.bd.sB[d] = sBt[d]; g.bd.sC[d] = sC[d];
+    }
+    g.batches = (uint32_t)batches;
+    if (cdims == 3 && sBt[0] == 0 && (uint64_t)sA[0] == (uint64_t)g.M * g.lda &&
+        (uint64_t)sC[0] == (uint64_t)g.M * g.ldc && batches > 1) {
+        g.M = (uint32_t)(batches * g.M);
+        g.batches = 1;
+        g.bd.n = 0;
+    }
+    hipStream_t st;
+    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+    switch (dtype) {
+    case MX_FLOAT32: return launch_mfma<MX_FLOAT32>(g, C, A, Bt, st);
+    case MX_FLOAT16: return launch_mfma<MX_FLOAT16>(g, C, A, Bt, st);
+    case MX_BFLOAT16: return launch_mfma<MX_BFLOAT16>(g, C, A, Bt, st);
+    case MX_INT32: return launch_scalar<MX_INT32>(g, C, A, Bt, st);
+    case MX_INT16: return launch_scalar<MX_INT16>(g, C, A, Bt, st);
+    case MX_INT8: return launch_scalar<MX_INT8>(g, C, A, Bt, st);
+    case MX_INT64: return launch_scalar<MX_INT64>(g, C, A, Bt, st);
+    case MX_UINT8: return launch_scalar<MX_UINT8>(g, C, A, Bt, st);
+    case MX_UINT16: return launch_scalar<MX_UINT16>(g, C, A, Bt, st);
+    case MX_UINT32: return launch_scalar<MX_UINT32>(g, C, A, Bt, st);
+    case MX_UINT64: return launch_scalar<MX_UINT64>(g, C, A, Bt, st);
+    case MX_BOOL: return launch_scalar<MX_BOOL>(g, C, A, Bt, st);
+    default:
+        return fail(MX_ERR_UNSUPPORTED, "mx_launch_batched_matmul: no kernel for dtype " + std::to_string(dtype));
+    }
+}

@@ -394,6 +394,8 @@ int orc_reduce(int op, int dtype, int acc_mode, uint32_t reduce_stride, uint32_t
 #define BF16_F32_FMA(acc, a, b) fmaf(orc_bf16_to_f32(a), orc_bf16_to_f32(b), (acc))
 #define INT_MAC(acc, a, b) ((acc) + (uint64_t)(int64_t)(a) * (uint64_t)(int64_t)(b))
 #define UINT_MAC(acc, a, b) ((acc) + (uint64_t)(a) * (uint64_t)(b))
+/* bool: sum + a * b is an int, stored back into the bool accumulator as (value != 0) */
+#define BOOL_MAC(acc, a, b) ((uint8_t)(((int)(acc) + (int)(a) * (int)(b)) != 0))
 
 int orc_batched_matmul(int dtype, int acc_mode, int cdims, const uint32_t* shape,
                        const uint32_t* sA, const uint32_t* sBt, const uint32_t* sC,
@@ -420,6 +422,7 @@ int orc_batched_matmul(int dtype, int acc_mode, int cdims, const uint32_t* shape
     case ORC_U16: MM_LOOP(uint16_t, uint64_t, UINT_MAC, (uint16_t)); return 0;
     case ORC_U32: MM_LOOP(uint32_t, uint64_t, UINT_MAC, (uint32_t)); return 0;
     case ORC_U64: MM_LOOP(uint64_t, uint64_t, UINT_MAC, (uint64_t)); return 0;
+    case ORC_BOOL: MM_LOOP(uint8_t, uint8_t, BOOL_MAC, IDENT); return 0;
     default: return -1;
     }
 }

@@ -1,0 +1,145 @@
+"""GPU parity: batched MatMul vs the oracle.
+
+fp32: normwise relative error <= 1e-4 against the oracle (the reference's sequential loop);
+fp16 / bf16 with fp32 accumulation: <= 1e-2 normwise against the oracle's fp32-accumulator mode
+(same loop, float accumulator, one rounding) -- the literal reference loop accumulates in half,
+whose own error at K = 2048 is about that large, so it is reported, not gated;
+integer dtypes: exact (wrap-around).  Descriptors come from the product's broadcast +
+collapse_dims_matmul helpers, as dot() builds them.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from helpers import contiguous_strides, normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def matmul_desc(mx, a_shape, a_strides, bt_shape, bt_strides):
+    out, out_st, b1s, b1st, b2s, b2st = mx.broadcast_shapes(a_shape, a_strides, bt_shape, bt_strides, matmul=True)
+    if len(out) == 2:
+        desc = [out, [b1st[0], b1st[1]], [b2st[0], b2st[1]], out_st]
+    else:
+        desc = mx.collapse_dims_matmul(out, b1st, b2st, out_st)
+    return out, desc
+
+
+def run_mm(mx, orc, code, a, bt, a_shape=None, a_strides=None, bt_shape=None, bt_strides=None, acc=None):
+    a_shape = list(a_shape or a.shape)
+    bt_shape = list(bt_shape or bt.shape)
+    a_strides = a_strides or contiguous_strides(a_shape)
+    bt_strides = bt_strides or contiguous_strides(bt_shape)
+    out, desc = matmul_desc(mx, a_shape, a_strides, bt_shape, bt_strides)
+    K = a_shape[-1]
+    total = int(np.prod(out))
+    A = mx.DeviceBuffer.from_numpy(a.reshape(-1))
+    B = mx.DeviceBuffer.from_numpy(bt.reshape(-1))
+    C = mx.DeviceBuffer(total * a.dtype.itemsize)
+    mx.launch_batched_matmul(code, desc, K, C.ptr, A.ptr, B.ptr)
+    mx.sync()
+    got = C.download(a.dtype, total)
+    ref = orc.batched_matmul(code, desc, K, a.reshape(-1), bt.reshape(-1), total,
+                             acc=orc.ACC_F32 if acc is None else acc)
+    return got, ref, out
+
+
+def as_f32(code, arr, mx):
+    if code == mx.BFLOAT16:
+        return (arr.astype(np.uint32) << 16).view(np.float32)
+    return arr.astype(np.float32)
+
+
+def gen(rng, code, shape, scale, mx):
+    x = (rng.standard_normal(shape) * scale).astype(np.float32)
+    if code == mx.FLOAT16:
+        return x.astype(np.float16)
+    if code == mx.BFLOAT16:
+        from oracle.oracle import f32_to_bf16_bits
+        return f32_to_bf16_bits(x)
+    return x
+
+
+TOL = {"FLOAT32": 1e-4, "FLOAT16": 1e-2, "BFLOAT16": 1e-2}
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
+    ([2, 300, 200], [2, 150, 200]),      # ragged M, N, K (tile edges, K tail)
+    ([3, 64, 64], [64, 64]),             # Bt broadcast over the batch (folds into M)
+    ([513, 257], [129, 257]),            # rank 2, odd sizes
+    ([2, 2, 40, 72], [2, 1, 24, 72]),    # two batch axes, one broadcast
+    ([1, 256, 512], [256, 512]),         # exact tiles
+])
+def test_float_matmul_shapes(mx, orc, dt, case):
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(10)
+    a_shape, bt_shape = case
+    K = a_shape[-1]
+    a = gen(rng, code, a_shape, 1.0 / math.sqrt(K), mx)
+    bt = gen(rng, code, bt_shape, 1.0, mx)
+    got, ref, _ = run_mm(mx, orc, code, a, bt)
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16"])
+def test_main_matmul_shape_reduced_batch(mx, orc, dt):
+    """A[2,2048,2048] x B[2048,2048] (B broadcast): the batched-matmul workload's shape at batch 2."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(0)
+    a = gen(rng, code, [2, 2048, 2048], 1.0 / math.sqrt(2048), mx)
+    bt = gen(rng, code, [2048, 2048], 1.0 / math.sqrt(2048), mx)
+    got, ref, _ = run_mm(mx, orc, code, a, bt)
+    err = normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx))
+    assert err <= TOL[dt], err
+
+
+def test_skinny_matmul(mx, orc):
+    """A[8,1,4096] x B[4096,4096]: the skinny case (memory bound)."""
+    rng = np.random.default_rng(1)
+    for code in (mx.FLOAT32, mx.FLOAT16):
+        a = gen(rng, code, [8, 1, 4096], 1.0 / 64, mx)
+        bt = gen(rng, code, [4096, 4096], 1.0 / 64, mx)
+        got, ref, out = run_mm(mx, orc, code, a, bt)
+        assert out == [8, 1, 4096]
+        tol = 1e-4 if code == mx.FLOAT32 else 1e-2
+        assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= tol
+
+
+def test_identity_and_one_hot_exact(mx, orc):
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal([3, 96, 80]).astype(np.float32)
+    eye = np.eye(80, dtype=np.float32)           # Bt = I  ->  C = A exactly
+    got, _, _ = run_mm(mx, orc, mx.FLOAT32, a, eye)
+    assert np.array_equal(got.reshape(3, 96, 80), a)
+    perm = np.eye(80, dtype=np.float32)[rng.permutation(80)]
+    got, _, _ = run_mm(mx, orc, mx.FLOAT32, a, perm)
+    assert np.array_equal(got.reshape(3, 96, 80), a @ perm.T)
+
+
+def test_strided_operands(mx, orc):
+    """Non-unit K stride (a transposed view) takes the scalar-load path."""
+    rng = np.random.default_rng(3)
+    base = rng.standard_normal([70, 50]).astype(np.float32)     # A = base.T : [50, 70], strides [1, 50]
+    bt = rng.standard_normal([30, 70]).astype(np.float32)
+    got, ref, _ = run_mm(mx, orc, mx.FLOAT32, base, bt, a_shape=[50, 70], a_strides=[1, 50])
+    ref64 = base.T.astype(np.float64) @ bt.T.astype(np.float64)
+    assert normwise_rel(got, ref64) <= 1e-5
+    del ref
+
+
+@pytest.mark.parametrize("dt", ["INT32", "INT8", "INT64", "UINT8", "UINT32", "INT16", "UINT16", "UINT64", "BOOL"])
+def test_integer_matmul_exact(mx, orc, dt):
+    code = getattr(mx, dt)
+    npt = mx.NP_DTYPE[code]
+    rng = np.random.default_rng(4)
+    if code == mx.BOOL:
+        a = rng.integers(0, 2, [2, 17, 9]).astype(np.bool_)
+        bt = rng.integers(0, 2, [2, 5, 9]).astype(np.bool_)
+    else:
+        info = np.iinfo(npt)
+        a = rng.integers(info.min, info.max, [2, 17, 9], dtype=npt, endpoint=True)
+        bt = rng.integers(info.min, info.max, [2, 5, 9], dtype=npt, endpoint=True)
+    got, ref, _ = run_mm(mx, orc, code, a, bt)
+    assert np.array_equal(got, ref)
