@@ -73,26 +73,36 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t nblocks, uint32_t 
 
 // Loads this thread's 8 chunks (16 B each) of a 256-row operand tile at K offset k0 into regs.
 // Chunk q = tid + 256 i covers row q / 8, bytes (q % 8) * 16 of that row's 128-byte K slice.
-template <typename S, bool VEC>
-__device__ __forceinline__ void load_tile(uint4 (&r)[8], const S* __restrict__ base, uint32_t rows_valid,
-                                          uint32_t ld, uint32_t kstride, uint32_t k0, uint32_t K) {
+// Full K step of K-contiguous rows: one 128-bit load per chunk, no branches.  Rows past the
+// operand's end re-read its last row (their products land only in C rows / columns that are
+// never stored).
+template <typename S>
+__device__ __forceinline__ void load_tile_full(uint4 (&r)[8], const S* __restrict__ base, uint32_t rows_valid,
+                                               uint32_t ld, uint32_t k0) {
     constexpr int CE = 16 / sizeof(S);    // elements per chunk
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int q = threadIdx.x + NTHREADS * i;
-        const int row = q >> 3, c = q & 7;
-        const uint32_t k = k0 + c * CE;
-        if (VEC && row < (int)rows_valid && k + CE <= K) {
-            r[i] = *reinterpret_cast<const uint4*>(base + (uint64_t)row * ld + k);
-        } else {
-            S tmp[CE];
+        const uint32_t row = min((uint32_t)(q >> 3), rows_valid - 1);
+        r[i] = *reinterpret_cast<const uint4*>(base + (uint64_t)row * ld + k0 + (q & 7) * CE);
+    }
+}
+
+// K tail or strided operands: element loads, zero past K (zeros keep the tail exact).
+template <typename S>
+__device__ __forceinline__ void load_tile_guarded(uint4 (&r)[8], const S* __restrict__ base, uint32_t rows_valid,
+                                                  uint32_t ld, uint32_t kstride, uint32_t k0, uint32_t K) {
+    constexpr int CE = 16 / sizeof(S);
 #pragma unroll
-            for (int e = 0; e < CE; e++) {
-                const bool ok = row < (int)rows_valid && k + e < K;
-                tmp[e] = ok ? base[(uint64_t)row * ld + (uint64_t)(k + e) * kstride] : S(0);
-            }
-            __builtin_memcpy(&r[i], tmp, 16);
-        }
+    for (int i = 0; i < 8; i++) {
+        const int q = threadIdx.x + NTHREADS * i;
+        const uint32_t row = min((uint32_t)(q >> 3), rows_valid - 1);
+        const uint32_t k = k0 + (q & 7) * CE;
+        S tmp[CE];
+#pragma unroll
+        for (int e = 0; e < CE; e++)
+            tmp[e] = (k + e < K) ? base[(uint64_t)row * ld + (uint64_t)(k + e) * kstride] : S(0);
+        __builtin_memcpy(&r[i], tmp, 16);
     }
 }
 
@@ -105,74 +115,91 @@ __device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[8]) {
     }
 }
 
+// One K step's operand fragments for one wave, read from LDS before any of the step's MFMAs.
+// 16-bit types: a K block is 16 elements = 2 chunks; lane half h holds chunk 2 kb + h of its row.
+// fp32: a K block is 16 elements = 4 chunks; lane half h holds chunks 4 kb + 2h, 4 kb + 2h + 1
+// (K offsets 8h .. 8h + 7); MFMA substep s consumes element s, so the two lane halves supply
+// k = s and k = 8 + s.
+template <int DT> struct Frags;
+template <> struct Frags<MX_FLOAT16> { static constexpr int KB = 4; h8v a[KB][4], b[KB][4]; };
+template <> struct Frags<MX_BFLOAT16> { static constexpr int KB = 4; b8v a[KB][4], b[KB][4]; };
+template <> struct Frags<MX_FLOAT32> { static constexpr int KB = 2; float4 a[KB][4][2], b[KB][4][2]; };
+
 template <int DT>
-__device__ __forceinline__ void mma_kblock(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
-                                           int wm, int wn, int lane);
-
-// 16-bit: one K block = 16 elements = 2 chunks; lane half h reads chunk 2 kb + h (8 elements).
-template <>
-__device__ __forceinline__ void mma_kblock<MX_FLOAT16>(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
-                                                       int wm, int wn, int lane) {
+__device__ __forceinline__ void read_frags(Frags<DT>& f, const char* la, const char* lb, int wm, int wn, int lane) {
     const int r32 = lane & 31, h = lane >> 5;
-    h8v a[4], b[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int ra = wm * 128 + t * 32 + r32;
-        const int rb = wn * 128 + t * 32 + r32;
-        a[t] = *reinterpret_cast<const h8v*>(la + ra * ROWB + swz(ra, 2 * kb + h) * 16);
-        b[t] = *reinterpret_cast<const h8v*>(lb + rb * ROWB + swz(rb, 2 * kb + h) * 16);
-    }
+    for (int kb = 0; kb < Frags<DT>::KB; kb++)
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int t = 0; t < 4; t++) {
+            const int ra = wm * 128 + t * 32 + r32;
+            const int rb = wn * 128 + t * 32 + r32;
+            if constexpr (DT == MX_FLOAT32) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int u = 0; u < 2; u++) {
+                    f.a[kb][t][u] = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 4 * kb + 2 * h + u) * 16);
+                    f.b[kb][t][u] = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 4 * kb + 2 * h + u) * 16);
+                }
+            } else {
+                using V = std::remove_reference_t<decltype(f.a[0][0])>;
+                f.a[kb][t] = *reinterpret_cast<const V*>(la + ra * ROWB + swz(ra, 2 * kb + h) * 16);
+                f.b[kb][t] = *reinterpret_cast<const V*>(lb + rb * ROWB + swz(rb, 2 * kb + h) * 16);
+            }
+        }
 }
 
-template <>
-__device__ __forceinline__ void mma_kblock<MX_BFLOAT16>(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
-                                                        int wm, int wn, int lane) {
-    const int r32 = lane & 31, h = lane >> 5;
-    b8v a[4], b[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int ra = wm * 128 + t * 32 + r32;
-        const int rb = wn * 128 + t * 32 + r32;
-        a[t] = *reinterpret_cast<const b8v*>(la + ra * ROWB + swz(ra, 2 * kb + h) * 16);
-        b[t] = *reinterpret_cast<const b8v*>(lb + rb * ROWB + swz(rb, 2 * kb + h) * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+__device__ __forceinline__ float f4_at(const float4 (&v)[2], int s) {
+    const float4& q = v[s >> 2];
+    switch (s & 3) { case 0: return q.x; case 1: return q.y; case 2: return q.z; default: return q.w; }
 }
 
-// fp32: one K block = 16 elements = 4 chunks; lane half h holds K offsets 8h..8h+7 (2 chunks)
-// and the 8 MFMA substeps s each consume element s: the two lane halves supply k = s and 8 + s.
-template <>
-__device__ __forceinline__ void mma_kblock<MX_FLOAT32>(f16v (&acc)[4][4], const char* la, const char* lb, int kb,
-                                                       int wm, int wn, int lane) {
-    const int r32 = lane & 31, h = lane >> 5;
-    float a[4][8], b[4][8];
+template <int DT>
+__device__ __forceinline__ void mma_step(f16v (&acc)[4][4], const Frags<DT>& f) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int ra = wm * 128 + t * 32 + r32;
-        const int rb = wn * 128 + t * 32 + r32;
-        const float4 a0 = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 4 * kb + 2 * h) * 16);
-        const float4 a1 = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 4 * kb + 2 * h + 1) * 16);
-        const float4 b0 = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 4 * kb + 2 * h) * 16);
-        const float4 b1 = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 4 * kb + 2 * h + 1) * 16);
-        a[t][0] = a0.x; a[t][1] = a0.y; a[t][2] = a0.z; a[t][3] = a0.w;
-        a[t][4] = a1.x; a[t][5] = a1.y; a[t][6] = a1.z; a[t][7] = a1.w;
-        b[t][0] = b0.x; b[t][1] = b0.y; b[t][2] = b0.z; b[t][3] = b0.w;
-        b[t][4] = b1.x; b[t][5] = b1.y; b[t][6] = b1.z; b[t][7] = b1.w;
+    for (int kb = 0; kb < Frags<DT>::KB; kb++) {
+        if constexpr (DT == MX_FLOAT32) {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_at(f.a[kb][i], s), f4_at(f.b[kb][j], s),
+                                                                        acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if constexpr (DT == MX_FLOAT16)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kb][i], f.b[kb][j], acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[kb][i], f.b[kb][j], acc[i][j], 0, 0, 0);
+                }
+        }
     }
-#pragma unroll
-    for (int s = 0; s < 8; s++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
 }
+
+// Direct global -> LDS copy of one operand's K step (gfx950 global_load_lds_dwordx4): the
+// wave's 8 instructions each fill 1 KB = 8 LDS rows; lane L lands at row 8p + L/8, physical
+// chunk L%8, so it fetches logical chunk (L%8) ^ (row & 7) = (L%8) ^ (L/8) of that row.
+template <typename S>
+__device__ __forceinline__ void dma_tile(char* lds, const S* __restrict__ base, uint32_t rows_valid, uint32_t ld,
+                                         uint32_t k0, int wave, int lane) {
+    constexpr int CE = 16 / sizeof(S);
+    const int c = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int p = wave * 8 + i;
+        const uint32_t row = min((uint32_t)(p * 8 + (lane >> 3)), rows_valid - 1);
+        const S* src = base + (uint64_t)row * ld + k0 + c * CE;
+        __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(lds + p * 1024),
+                                         16, 0, 0);
+    }
+}
+
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maximum): this wave's LDS DMA has landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 template <int DT, bool VEC>
 __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<DT>::S* __restrict__ C,
@@ -220,31 +247,62 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
     const uint32_t KT = (g.K + KSTEP - 1) / KSTEP;
-    uint4 ra[8], rb[8];
-    load_tile<S, VEC>(ra, Ablk, rows_a, g.lda, g.ka, 0, g.K);
-    load_tile<S, VEC>(rb, Bblk, rows_b, g.ldb, g.kb, 0, g.K);
-    store_tile(lds_a(0), ra);
-    store_tile(lds_b(0), rb);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < KT; kt++) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < KT;
-        if (more) {
-            load_tile<S, VEC>(ra, Ablk, rows_a, g.lda, g.ka, (kt + 1) * KSTEP, g.K);
-            load_tile<S, VEC>(rb, Bblk, rows_b, g.ldb, g.kb, (kt + 1) * KSTEP, g.K);
+    const uint32_t KT_full = VEC ? g.K / KSTEP : 0;     // whole K steps copied by LDS DMA
+    Frags<DT> f;
+    // Main loop: per step, read every fragment of the current stage, start the DMA of the next
+    // step into the other stage, then run the step's MFMAs while that DMA is in flight.
+    if (KT_full > 0) {
+        dma_tile<S>(lds_a(0), Ablk, rows_a, g.lda, 0, wave, lane);
+        dma_tile<S>(lds_b(0), Bblk, rows_b, g.ldb, 0, wave, lane);
+        wait_vmem();
+        __syncthreads();
+        for (uint32_t kt = 0; kt < KT_full; kt++) {
+            const int cur = kt & 1;
+            read_frags<DT>(f, lds_a(cur), lds_b(cur), wm, wn, lane);
+            if (kt + 1 < KT_full) {
+                dma_tile<S>(lds_a(cur ^ 1), Ablk, rows_a, g.lda, (kt + 1) * KSTEP, wave, lane);
+                dma_tile<S>(lds_b(cur ^ 1), Bblk, rows_b, g.ldb, (kt + 1) * KSTEP, wave, lane);
+            }
+            mma_step<DT>(acc, f);
+            wait_vmem();
+            __syncthreads();
         }
-#pragma unroll
-        for (int kb = 0; kb < KBLOCKS; kb++) mma_kblock<DT>(acc, lds_a(cur), lds_b(cur), kb, wm, wn, lane);
-        if (more) {
-            store_tile(lds_a(cur ^ 1), ra);
-            store_tile(lds_b(cur ^ 1), rb);
-        }
+    }
+    // K tail (and every step of strided operands): element loads through registers, zero past K.
+    for (uint32_t kt = KT_full; kt < KT; kt++) {
+        uint4 ra[8], rb[8];
+        load_tile_guarded<S>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, g.K);
+        load_tile_guarded<S>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, g.K);
+        store_tile(lds_a(0), ra);
+        store_tile(lds_b(0), rb);
+        __syncthreads();
+        read_frags<DT>(f, lds_a(0), lds_b(0), wm, wn, lane);
+        mma_step<DT>(acc, f);
         __syncthreads();
     }
 
     // epilogue: acc[i][j][r] is C[row, col] with row = 32 i + 8 (r / 4) + 4 h + r % 4, col = 32 j + lane % 32
     S* Cblk = C + offC;
     const int h = lane >> 5, c32 = lane & 31;
+    auto cvt = [](float v) -> S {
+        if constexpr (DT == MX_FLOAT32) return v;
+        else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
+        else return float_to_bf16(v);
+    };
+    if (m0 + BM <= g.M && n0 + BN <= g.N) {          // interior tile: no bounds checks
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t col = n0 + wn * 128 + j * 32 + c32;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                    Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = cvt(acc[i][j][r]);
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -254,14 +312,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint32_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                if (row < g.M) {
-                    const float v = acc[i][j][r];
-                    S o;
-                    if constexpr (DT == MX_FLOAT32) o = v;
-                    else if constexpr (DT == MX_FLOAT16) o = float_to_half_bits(v);
-                    else o = float_to_bf16(v);
-                    Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = o;
-                }
+                if (row < g.M) Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = cvt(acc[i][j][r]);
             }
         }
 }
