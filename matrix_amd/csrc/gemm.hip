@@ -11,11 +11,13 @@
 //                     reference's `T sum` loop does (Matrix.mm:7187-7191).
 //
 // Tiling (MFMA path): a 256-thread block computes a 256 x 256 tile of C as 2 x 2 waves of
-// 128 x 128 (4 x 4 MFMA tiles of 32 x 32, 256 fp32 accumulators per lane).  Each K step stages
-// 256 rows x 128 bytes of A and of Bt in LDS (64 elements of 16-bit data, 32 of fp32), double
-// buffered: the next step's global loads are in flight while the current step's MFMAs run.
-// LDS rows are 8 chunks of 16 bytes; chunk c of row r lives at c ^ (r & 7) so that the 32 rows
-// one MFMA operand read touches spread over all banks.
+// 128 x 128 (4 x 4 MFMA tiles of 32 x 32, 256 fp32 accumulators per lane).  A K step stages
+// 256 rows x 64 bytes of A and of Bt in LDS (32 elements of 16-bit data, 16 of fp32).  Four
+// stages form a ring: direct global -> LDS loads (gfx950 global_load_lds_dwordx4) run three
+// steps ahead of the MFMAs, and each step first reads all of its fragments, then starts the
+// DMA three steps ahead, then issues its MFMAs.  Each stage is its own __shared__ array, so the
+// compiler can tell the DMA into one stage from the reads of another and adds no waits of its own.
+// LDS rows are 4 chunks of 16 bytes, swizzled so that one MFMA operand read is bank-conflict free.
 // Block ids are remapped so that the tiles one XCD (one L2) runs are consecutive M panels with
 // all their N tiles: each A panel is fetched into an L2 once and reused across N.
 // When Bt is shared by the whole batch (batch stride 0) and A / C stack their batches
@@ -30,10 +32,13 @@ typedef __bf16 b8v __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 256, BN = 256;
-constexpr int ROWB = 128;                 // bytes of one LDS tile row per K step
+constexpr int ROWB = 64;                  // bytes of one LDS tile row per K step
+constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
 constexpr int NTHREADS = 256;
-constexpr int STAGE_BYTES = BM * ROWB;    // one operand, one stage: 32 KB
+constexpr int STAGE_BYTES = BM * ROWB;    // one operand, one stage: 16 KB
+constexpr int NSTAGES = 4;
 constexpr int NUM_XCD = 8;
+constexpr int DMA_PER_WAVE = STAGE_BYTES / 1024 / 4;   // 1 KB DMA instructions per wave per operand
 
 template <int DT> struct MmaTraits;
 template <> struct MmaTraits<MX_FLOAT16> { using S = uint16_t; };
@@ -55,7 +60,11 @@ struct GemmArgs {
     BatchDesc bd;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+// LDS swizzle: logical chunk c of row r is stored at c ^ ((r >> 2) & 3).  The LDS serves a
+// 128-bit read 16 lanes (256 bytes, 64 banks) at a time; one MFMA operand read has 16 lanes on
+// 16 consecutive rows with the same logical chunk, whose 16-byte bank groups
+// 4 (r % 4) + stored chunk are then all distinct.
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
 
 // Block id -> (batch, tile_m, tile_n).  Hardware dispatch hands block i to XCD i % 8; the
 // remap gives each XCD a contiguous run of logical tiles, ordered M panel by M panel.
@@ -71,33 +80,19 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t nblocks, uint32_t 
     tn = t - tm * tiles_n;
 }
 
-// Loads this thread's 8 chunks (16 B each) of a 256-row operand tile at K offset k0 into regs.
-// Chunk q = tid + 256 i covers row q / 8, bytes (q % 8) * 16 of that row's 128-byte K slice.
-// Full K step of K-contiguous rows: one 128-bit load per chunk, no branches.  Rows past the
-// operand's end re-read its last row (their products land only in C rows / columns that are
-// never stored).
+// K tail or strided operands: this thread's 4 chunks of a 256-row tile through registers,
+// element loads, zero past K (zeros keep the tail exact).  Chunk q = tid + 256 i is row q / 4,
+// logical chunk q % 4.  Rows past the operand's end re-read its last row (their products land
+// only in C rows / columns that are never stored).
 template <typename S>
-__device__ __forceinline__ void load_tile_full(uint4 (&r)[8], const S* __restrict__ base, uint32_t rows_valid,
-                                               uint32_t ld, uint32_t k0) {
-    constexpr int CE = 16 / sizeof(S);    // elements per chunk
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int q = threadIdx.x + NTHREADS * i;
-        const uint32_t row = min((uint32_t)(q >> 3), rows_valid - 1);
-        r[i] = *reinterpret_cast<const uint4*>(base + (uint64_t)row * ld + k0 + (q & 7) * CE);
-    }
-}
-
-// K tail or strided operands: element loads, zero past K (zeros keep the tail exact).
-template <typename S>
-__device__ __forceinline__ void load_tile_guarded(uint4 (&r)[8], const S* __restrict__ base, uint32_t rows_valid,
+__device__ __forceinline__ void load_tile_guarded(uint4 (&r)[4], const S* __restrict__ base, uint32_t rows_valid,
                                                   uint32_t ld, uint32_t kstride, uint32_t k0, uint32_t K) {
     constexpr int CE = 16 / sizeof(S);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < 4; i++) {
         const int q = threadIdx.x + NTHREADS * i;
-        const uint32_t row = min((uint32_t)(q >> 3), rows_valid - 1);
-        const uint32_t k = k0 + (q & 7) * CE;
+        const uint32_t row = min((uint32_t)(q / CPR), rows_valid - 1);
+        const uint32_t k = k0 + (q % CPR) * CE;
         S tmp[CE];
 #pragma unroll
         for (int e = 0; e < CE; e++)
@@ -106,24 +101,24 @@ __device__ __forceinline__ void load_tile_guarded(uint4 (&r)[8], const S* __rest
     }
 }
 
-__device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[8]) {
+__device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[4]) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < 4; i++) {
         const int q = threadIdx.x + NTHREADS * i;
-        const int row = q >> 3, c = q & 7;
+        const int row = q / CPR, c = q % CPR;
         *reinterpret_cast<uint4*>(lds + row * ROWB + swz(row, c) * 16) = r[i];
     }
 }
 
 // One K step's operand fragments for one wave, read from LDS before any of the step's MFMAs.
 // 16-bit types: a K block is 16 elements = 2 chunks; lane half h holds chunk 2 kb + h of its row.
-// fp32: a K block is 16 elements = 4 chunks; lane half h holds chunks 4 kb + 2h, 4 kb + 2h + 1
+// fp32: the step is one K block of 16 elements = 4 chunks; lane half h holds chunks 2h, 2h + 1
 // (K offsets 8h .. 8h + 7); MFMA substep s consumes element s, so the two lane halves supply
 // k = s and k = 8 + s.
 template <int DT> struct Frags;
-template <> struct Frags<MX_FLOAT16> { static constexpr int KB = 4; h8v a[KB][4], b[KB][4]; };
-template <> struct Frags<MX_BFLOAT16> { static constexpr int KB = 4; b8v a[KB][4], b[KB][4]; };
-template <> struct Frags<MX_FLOAT32> { static constexpr int KB = 2; float4 a[KB][4][2], b[KB][4][2]; };
+template <> struct Frags<MX_FLOAT16> { static constexpr int KB = 2; h8v a[KB][4], b[KB][4]; };
+template <> struct Frags<MX_BFLOAT16> { static constexpr int KB = 2; b8v a[KB][4], b[KB][4]; };
+template <> struct Frags<MX_FLOAT32> { static constexpr int KB = 1; float4 a[KB][4][2], b[KB][4][2]; };
 
 template <int DT>
 __device__ __forceinline__ void read_frags(Frags<DT>& f, const char* la, const char* lb, int wm, int wn, int lane) {
@@ -137,8 +132,8 @@ __device__ __forceinline__ void read_frags(Frags<DT>& f, const char* la, const c
             if constexpr (DT == MX_FLOAT32) {
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
-                    f.a[kb][t][u] = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 4 * kb + 2 * h + u) * 16);
-                    f.b[kb][t][u] = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 4 * kb + 2 * h + u) * 16);
+                    f.a[kb][t][u] = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, 2 * h + u) * 16);
+                    f.b[kb][t][u] = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, 2 * h + u) * 16);
                 }
             } else {
                 using V = std::remove_reference_t<decltype(f.a[0][0])>;
@@ -153,6 +148,9 @@ __device__ __forceinline__ float f4_at(const float4 (&v)[2], int s) {
     switch (s & 3) { case 0: return q.x; case 1: return q.y; case 2: return q.z; default: return q.w; }
 }
 
+// The Bt fragment goes in the MFMA's first operand slot and the A fragment in the second, so
+// the 32 x 32 result is the C^T tile: lane l holds C row (l % 32) and, in acc[4 q .. 4 q + 3],
+// the 4 consecutive C columns 8 q + 4 (l / 32) .. + 3 -- one vector store per (q) in the epilogue.
 template <int DT>
 __device__ __forceinline__ void mma_step(f16v (&acc)[4][4], const Frags<DT>& f) {
 #pragma unroll
@@ -164,7 +162,7 @@ __device__ __forceinline__ void mma_step(f16v (&acc)[4][4], const Frags<DT>& f) 
                 for (int i = 0; i < 4; i++)
 #pragma unroll
                     for (int j = 0; j < 4; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_at(f.a[kb][i], s), f4_at(f.b[kb][j], s),
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_at(f.b[kb][j], s), f4_at(f.a[kb][i], s),
                                                                         acc[i][j], 0, 0, 0);
         } else {
 #pragma unroll
@@ -172,34 +170,48 @@ __device__ __forceinline__ void mma_step(f16v (&acc)[4][4], const Frags<DT>& f) 
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     if constexpr (DT == MX_FLOAT16)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kb][i], f.b[kb][j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[kb][j], f.a[kb][i], acc[i][j], 0, 0, 0);
                     else
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[kb][i], f.b[kb][j], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[kb][j], f.a[kb][i], acc[i][j], 0, 0, 0);
                 }
         }
     }
 }
 
-// Direct global -> LDS copy of one operand's K step (gfx950 global_load_lds_dwordx4): the
-// wave's 8 instructions each fill 1 KB = 8 LDS rows; lane L lands at row 8p + L/8, physical
-// chunk L%8, so it fetches logical chunk (L%8) ^ (row & 7) = (L%8) ^ (L/8) of that row.
+// Direct global -> LDS copy of one operand's K step: the wave's DMA_PER_WAVE instructions each
+// fill 1 KB = 16 LDS rows; lane L lands at row r = 16 p + L / 4, stored chunk L % 4, so it
+// fetches the logical chunk that swz() stores there (swz is its own inverse).
 template <typename S>
 __device__ __forceinline__ void dma_tile(char* lds, const S* __restrict__ base, uint32_t rows_valid, uint32_t ld,
                                          uint32_t k0, int wave, int lane) {
     constexpr int CE = 16 / sizeof(S);
-    const int c = (lane & 7) ^ (lane >> 3);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int p = wave * 8 + i;
-        const uint32_t row = min((uint32_t)(p * 8 + (lane >> 3)), rows_valid - 1);
+    for (int i = 0; i < DMA_PER_WAVE; i++) {
+        const int p = wave * DMA_PER_WAVE + i;
+        const int r = p * 16 + lane / CPR;
+        const int c = swz(r, lane % CPR);
+        const uint32_t row = min((uint32_t)r, rows_valid - 1);
         const S* src = base + (uint64_t)row * ld + k0 + c * CE;
         __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(lds + p * 1024),
                                          16, 0, 0);
     }
 }
 
-// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maximum): this wave's LDS DMA has landed.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N), expcnt / lgkmcnt left at their maximum (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Workgroup barrier for the DMA ring.  __syncthreads() carries a workgroup release fence that
+// waits for every outstanding vector-memory operation -- including the DMA of later steps that
+// is meant to stay in flight.  The ring orders its LDS traffic itself: each wave waits (vmcnt)
+// for the DMA of the step it is about to read, and a stage is overwritten only after the
+// barrier that follows every wave's reads of it (lgkmcnt(0): this wave's reads have returned).
+// The memory clobber keeps the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int DT, bool VEC>
 __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<DT>::S* __restrict__ C,
@@ -208,16 +220,24 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<
                                                              GemmArgs g) {
     using S = typename MmaTraits<DT>::S;
     constexpr int KSTEP = ROWB / sizeof(S);            // elements of K per LDS stage
-    constexpr int KBLOCKS = KSTEP / 16;
-    extern __shared__ __align__(16) char smem[];
-    // stage s of A at smem + s * STAGE_BYTES, of Bt at smem + (2 + s) * STAGE_BYTES
-    auto lds_a = [&](int s) { return smem + s * STAGE_BYTES; };
-    auto lds_b = [&](int s) { return smem + (2 + s) * STAGE_BYTES; };
+    __shared__ __align__(16) char la0[STAGE_BYTES], la1[STAGE_BYTES], la2[STAGE_BYTES], la3[STAGE_BYTES];
+    __shared__ __align__(16) char lb0[STAGE_BYTES], lb1[STAGE_BYTES], lb2[STAGE_BYTES], lb3[STAGE_BYTES];
+    auto stage_a = [&](auto st) -> char* {
+        if constexpr (decltype(st)::value == 0) return la0;
+        else if constexpr (decltype(st)::value == 1) return la1;
+        else if constexpr (decltype(st)::value == 2) return la2;
+        else return la3;
+    };
+    auto stage_b = [&](auto st) -> char* {
+        if constexpr (decltype(st)::value == 0) return lb0;
+        else if constexpr (decltype(st)::value == 1) return lb1;
+        else if constexpr (decltype(st)::value == 2) return lb2;
+        else return lb3;
+    };
 
     uint32_t bidx, tm, tn;
     tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, bidx, tm, tn);
-    // batch offsets
-    uint64_t offA = 0, offB = 0, offC = 0;
+    uint64_t offA = 0, offB = 0, offC = 0;                // batch offsets
     {
         uint32_t rem = bidx;
         for (int d = g.bd.n - 1; d >= 0; --d) {
@@ -249,39 +269,73 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<
     const uint32_t KT = (g.K + KSTEP - 1) / KSTEP;
     const uint32_t KT_full = VEC ? g.K / KSTEP : 0;     // whole K steps copied by LDS DMA
     Frags<DT> f;
-    // Main loop: per step, read every fragment of the current stage, start the DMA of the next
-    // step into the other stage, then run the step's MFMAs while that DMA is in flight.
+    auto dma_step = [&](auto st, uint32_t kt) {
+        dma_tile<S>(stage_a(st), Ablk, rows_a, g.lda, kt * KSTEP, wave, lane);
+        dma_tile<S>(stage_b(st), Bblk, rows_b, g.ldb, kt * KSTEP, wave, lane);
+    };
+    // One pipelined step kt in stage ST (= kt % 4): wait for its DMA (steps kt+1, kt+2 may stay
+    // in flight), barrier, read all fragments, start the DMA of step kt + 3 into the stage the
+    // previous step just finished reading, then run the MFMAs.
+    constexpr int PER_STEP = 2 * DMA_PER_WAVE;           // DMA instructions per wave per step
+    // steady state: every step has two later steps in flight and issues the one three ahead --
+    // no branches, so the compiler's own wait bookkeeping stays exact
+    auto steady = [&](auto st, uint32_t kt) {
+        constexpr int ST = decltype(st)::value;
+        wait_vmem<2 * PER_STEP>();
+        ring_barrier();
+        read_frags<DT>(f, stage_a(st), stage_b(st), wm, wn, lane);
+        dma_step(std::integral_constant<int, (ST + 3) % NSTAGES>{}, kt + 3);
+        mma_step<DT>(acc, f);
+    };
+    // the last steps: fewer DMAs in flight, none issued past the end
+    auto drain = [&](auto st, uint32_t kt) {
+        constexpr int ST = decltype(st)::value;
+        if (kt >= KT_full) return;
+        if (kt + 2 < KT_full) wait_vmem<2 * PER_STEP>();
+        else if (kt + 1 < KT_full) wait_vmem<PER_STEP>();
+        else wait_vmem<0>();
+        ring_barrier();
+        read_frags<DT>(f, stage_a(st), stage_b(st), wm, wn, lane);
+        if (kt + 3 < KT_full) dma_step(std::integral_constant<int, (ST + 3) % NSTAGES>{}, kt + 3);
+        mma_step<DT>(acc, f);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
     if (KT_full > 0) {
-        dma_tile<S>(lds_a(0), Ablk, rows_a, g.lda, 0, wave, lane);
-        dma_tile<S>(lds_b(0), Bblk, rows_b, g.ldb, 0, wave, lane);
-        wait_vmem();
-        __syncthreads();
-        for (uint32_t kt = 0; kt < KT_full; kt++) {
-            const int cur = kt & 1;
-            read_frags<DT>(f, lds_a(cur), lds_b(cur), wm, wn, lane);
-            if (kt + 1 < KT_full) {
-                dma_tile<S>(lds_a(cur ^ 1), Ablk, rows_a, g.lda, (kt + 1) * KSTEP, wave, lane);
-                dma_tile<S>(lds_b(cur ^ 1), Bblk, rows_b, g.ldb, (kt + 1) * KSTEP, wave, lane);
-            }
-            mma_step<DT>(acc, f);
-            wait_vmem();
-            __syncthreads();
+        dma_step(I0{}, 0);
+        if (KT_full > 1) dma_step(I1{}, 1);
+        if (KT_full > 2) dma_step(I2{}, 2);
+        // Eight steps (two turns of the ring) per iteration: the compiler's wait bookkeeping loses
+        // track of which stage the in-flight DMA targets across the loop back edge and drains it
+        // there, so the back edge is kept rare.
+        uint32_t kt = 0;
+        for (; kt + 11 <= KT_full; kt += 2 * NSTAGES) {   // steps kt .. kt+7 issue kt+3 .. kt+10
+            steady(I0{}, kt);     steady(I1{}, kt + 1); steady(I2{}, kt + 2); steady(I3{}, kt + 3);
+            steady(I0{}, kt + 4); steady(I1{}, kt + 5); steady(I2{}, kt + 6); steady(I3{}, kt + 7);
         }
+        // kt is a multiple of 4 here; at most 10 steps remain
+        drain(I0{}, kt);     drain(I1{}, kt + 1); drain(I2{}, kt + 2); drain(I3{}, kt + 3);
+        drain(I0{}, kt + 4); drain(I1{}, kt + 5); drain(I2{}, kt + 6); drain(I3{}, kt + 7);
+        drain(I0{}, kt + 8); drain(I1{}, kt + 9);
+        __syncthreads();                                  // every wave is done with the ring
     }
     // K tail (and every step of strided operands): element loads through registers, zero past K.
     for (uint32_t kt = KT_full; kt < KT; kt++) {
-        uint4 ra[8], rb[8];
+        uint4 ra[4], rb[4];
         load_tile_guarded<S>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, g.K);
         load_tile_guarded<S>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, g.K);
-        store_tile(lds_a(0), ra);
-        store_tile(lds_b(0), rb);
+        store_tile(la0, ra);
+        store_tile(lb0, rb);
         __syncthreads();
-        read_frags<DT>(f, lds_a(0), lds_b(0), wm, wn, lane);
+        read_frags<DT>(f, la0, lb0, wm, wn, lane);
         mma_step<DT>(acc, f);
         __syncthreads();
     }
 
-    // epilogue: acc[i][j][r] is C[row, col] with row = 32 i + 8 (r / 4) + 4 h + r % 4, col = 32 j + lane % 32
+    // epilogue: acc[i][j][4 q + e] is C[row, col] with row = 32 i + lane % 32 and
+    // col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
     S* Cblk = C + offC;
     const int h = lane >> 5, c32 = lane & 31;
     auto cvt = [](float v) -> S {
@@ -289,32 +343,42 @@ __global__ __launch_bounds__(NTHREADS) void gemm_mfma_kernel(typename MmaTraits<
         else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
         else return float_to_bf16(v);
     };
-    if (m0 + BM <= g.M && n0 + BN <= g.N) {          // interior tile: no bounds checks
+    const bool vec_store = g.cn == 1 && (g.ldc * sizeof(S)) % 16 == 0 && ((uintptr_t)Cblk % 16) == 0;
+    if (m0 + BM <= g.M && n0 + BN <= g.N && vec_store) {   // interior tile: 4 columns per store
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 4; i++) {
+            const uint32_t row = m0 + wm * 128 + i * 32 + c32;
+            S* crow = Cblk + (uint64_t)row * g.ldc + n0 + wn * 128 + 4 * h;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t col = n0 + wn * 128 + j * 32 + c32;
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const uint32_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                    Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = cvt(acc[i][j][r]);
+                for (int q = 0; q < 4; q++) {
+                    S* p = crow + j * 32 + 8 * q;
+                    if constexpr (DT == MX_FLOAT32) {
+                        *reinterpret_cast<float4*>(p) =
+                            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                    } else {
+                        uint2 v;
+                        v.x = (uint32_t)cvt(acc[i][j][4 * q]) | ((uint32_t)cvt(acc[i][j][4 * q + 1]) << 16);
+                        v.y = (uint32_t)cvt(acc[i][j][4 * q + 2]) | ((uint32_t)cvt(acc[i][j][4 * q + 3]) << 16);
+                        *reinterpret_cast<uint2*>(p) = v;
+                    }
                 }
-            }
+        }
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = m0 + wm * 128 + i * 32 + c32;
+        if (row >= g.M) continue;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t col = n0 + wn * 128 + j * 32 + c32;
-            if (col >= g.N) continue;
+        for (int j = 0; j < 4; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const uint32_t row = m0 + wm * 128 + i * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                if (row < g.M) Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = cvt(acc[i][j][r]);
+                const uint32_t col = n0 + wn * 128 + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                if (col < g.N) Cblk[(uint64_t)row * g.ldc + (uint64_t)col * g.cn] = cvt(acc[i][j][r]);
             }
-        }
+    }
 }
 
 // Scalar kernel for integer (and bool) dtypes: one output per thread, K loop in the element
@@ -368,26 +432,12 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t
     g.tiles_n = (g.N + BN - 1) / BN;
     const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches;
     if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: grid too large");
-    const size_t lds = 4 * STAGE_BYTES;
-    if (vec) {
-        static bool attr_set = false;
-        if (!attr_set) {
-            MX_HIP(hipFuncSetAttribute((const void*)gemm_mfma_kernel<DT, true>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            attr_set = true;
-        }
-        hipLaunchKernelGGL((gemm_mfma_kernel<DT, true>), dim3((uint32_t)blocks), dim3(NTHREADS), lds, st,
+    if (vec)
+        hipLaunchKernelGGL((gemm_mfma_kernel<DT, true>), dim3((uint32_t)blocks), dim3(NTHREADS), 0, st,
                            (S*)C, (const S*)A, (const S*)Bt, g);
-    } else {
-        static bool attr_set = false;
-        if (!attr_set) {
-            MX_HIP(hipFuncSetAttribute((const void*)gemm_mfma_kernel<DT, false>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            attr_set = true;
-        }
-        hipLaunchKernelGGL((gemm_mfma_kernel<DT, false>), dim3((uint32_t)blocks), dim3(NTHREADS), lds, st,
+    else
+        hipLaunchKernelGGL((gemm_mfma_kernel<DT, false>), dim3((uint32_t)blocks), dim3(NTHREADS), 0, st,
                            (S*)C, (const S*)A, (const S*)Bt, g);
-    }
     MX_HIP(hipGetLastError());
     return MX_OK;
 }
