@@ -84,27 +84,17 @@ _SIGS = {
     "mx_collapse_dims_reduce2": ([_u32p, _u32p, _u32p, _u32, _i, _i, _i, _u64, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_broadcast_shapes": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_broadcast_shapes_matmul": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
+    "mx_launch_batched_matmul": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp], _i),
+    "mx_conv_workspace_bytes": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _i, ctypes.POINTER(_sz)], _i),
+    "mx_launch_conv_nd": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _ip, _ip, _ip, _ip,
+                           _i, _i, _vp, _vp, _vp, _vp, _sz, _vp], _i),
+    "mx_launch_copy_strided": ([_i, _i, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp], _i),
 }
-_OPTIONAL = {"mx_launch_batched_matmul", "mx_launch_conv_nd", "mx_conv_workspace_bytes", "mx_launch_copy_strided"}
 
 for _name, (_args, _res) in _SIGS.items():
     _f = getattr(lib, _name)
     _f.argtypes = _args
     _f.restype = _res
-
-if hasattr(lib, "mx_launch_batched_matmul"):
-    lib.mx_launch_batched_matmul.argtypes = [_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp]
-    lib.mx_launch_batched_matmul.restype = _i
-if hasattr(lib, "mx_conv_workspace_bytes"):
-    lib.mx_conv_workspace_bytes.argtypes = [_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _i, ctypes.POINTER(_sz)]
-    lib.mx_conv_workspace_bytes.restype = _i
-if hasattr(lib, "mx_launch_conv_nd"):
-    lib.mx_launch_conv_nd.argtypes = [_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _ip, _ip, _ip, _ip,
-                                      _i, _i, _vp, _vp, _vp, _vp, _sz, _vp]
-    lib.mx_launch_conv_nd.restype = _i
-if hasattr(lib, "mx_launch_copy_strided"):
-    lib.mx_launch_copy_strided.argtypes = [_i, _i, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp]
-    lib.mx_launch_copy_strided.restype = _i
 
 
 def last_error() -> str:
@@ -302,3 +292,37 @@ def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=
     shape, sOut, sIn = desc
     check(lib.mx_launch_reduce(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn),
                                int(out), int(inp), int(workspace), workspace_bytes, stream))
+
+
+def conv_workspace_bytes(dtype, geom):
+    """geom = dict(in_shape, k_shape, out_shape, in_strides, k_strides, out_strides, groups, ...)."""
+    nb = ctypes.c_size_t()
+    ns = len(geom["in_shape"]) - 2
+    check(lib.mx_conv_workspace_bytes(dtype, ns, u32(geom["in_shape"]), u32(geom["k_shape"]),
+                                      u32(geom["out_shape"]), u32(geom["in_strides"]), u32(geom["k_strides"]),
+                                      u32(geom["out_strides"]), int(geom.get("groups", 1)), ctypes.byref(nb)))
+    return nb.value
+
+
+def launch_conv_nd(dtype, geom, out, inp, kern, workspace=0, workspace_bytes=0, stream=None):
+    """Channels-last N-D convolution (conv_gpu's argument set).  geom holds in_shape
+    [N, S.., C], k_shape [O, K.., C/groups], out_shape [N, O.., O], the three stride lists,
+    pad, stride, dil (kernel), dil_lhs (input), groups and flip; missing geometry defaults to
+    pad 0, stride 1, dilation 1, groups 1, no flip."""
+    ns = len(geom["in_shape"]) - 2
+    pad = geom.get("pad", [0] * ns)
+    stride = geom.get("stride", [1] * ns)
+    dil = geom.get("dil", [1] * ns)
+    dil_lhs = geom.get("dil_lhs", [1] * ns)
+    check(lib.mx_launch_conv_nd(dtype, ns, u32(geom["in_shape"]), u32(geom["k_shape"]), u32(geom["out_shape"]),
+                                u32(geom["in_strides"]), u32(geom["k_strides"]), u32(geom["out_strides"]),
+                                i32(pad), i32(stride), i32(dil), i32(dil_lhs), int(geom.get("groups", 1)),
+                                int(geom.get("flip", 0)), int(out), int(inp), int(kern), int(workspace),
+                                workspace_bytes, stream))
+
+
+def launch_copy_strided(dst_dtype, src_dtype, desc, dst, src, stream=None):
+    """desc = (shape, sDst, sSrc) over a collapsed iteration space (empty shape: one element)."""
+    shape, sDst, sSrc = desc
+    check(lib.mx_launch_copy_strided(dst_dtype, src_dtype, len(shape), u32(shape), u32(sDst), u32(sSrc),
+                                     int(dst), int(src), stream))

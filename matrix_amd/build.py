@@ -1,7 +1,9 @@
 """Builds the gfx950 kernel library (and the oracle when asked) in-tree.
 
-    python -m matrix_amd.build            # kernels -> matrix_amd/_lib/libmatrix_amd.so
-    python -m matrix_amd.build --oracle   # also oracle/_build/liboracle.so
+    python matrix_amd/build.py            # kernels -> matrix_amd/_lib/libmatrix_amd.so
+    python matrix_amd/build.py --oracle   # also oracle/_build/liboracle.so
+
+(Run by path: importing the package loads the library, which may be stale or absent.)
 
 Objects are compiled in parallel with hipcc for gfx950 only; packed-fp32 instructions are
 disabled for all device code.

@@ -1,0 +1,609 @@
+// conv.hip -- ConvolutionND, channels-last, as an implicit GEMM on the matrix cores.
+//
+// Replaces conv_gpu / conv2d_gpu (Matrix.mm:12335-12395, Matrix.mm:5521-5559) and their Metal
+// kernels (ConvolutionND.metal:18-372).  The semantics are those of the reference's CPU conv
+// (conv_cpu, Matrix.mm:12397-12500 == conv2d_cpu, Matrix.mm:5668-5741): input [N, S1..Sn, C],
+// kernel [O, K1..Kn, C / groups], output [N, O1..On, O], each with arbitrary element strides;
+// output position o samples input position o * stride - pad_lo + k * dil_rhs of the input
+// dilated by dil_lhs (taps off the image or between dilated samples contribute nothing); output
+// channel oc uses input channels of group oc / (O / groups); flip reads the kernel back to
+// front.  The reduction runs over (kernel position, channel), channel fastest.
+//
+// float32 / float16 / bfloat16, 1 or 2 spatial axes, no input dilation: implicit GEMM.
+//   C[m, o] = sum_k A[m, k] Wp[o, k] with m = (n, o1.., on) and k = (kernel position, channel).
+//   The image is packed (when it is not already so) into channels-last Xp [N, S.., groups, Cgp]
+//   and the kernel into Wp [O, K.., Cgp], Cgp = C / groups rounded up to a 128-byte K pair with
+//   zero channels, flip applied.  Every K pair then lies inside one kernel position, so the A
+//   tile's DMA gathers whole 128-byte channel runs straight from Xp: one address per lane per
+//   DMA instruction, a zero page for taps outside the image.  Groups are the GEMM batch.
+// Everything else (integers, input dilation, 3+ spatial axes): a direct kernel, one output per
+//   thread, in the reference's loop order (fp32 results then equal the CPU's bit for bit).
+#include "mfma_tile.hpp"
+
+namespace mx {
+namespace {
+
+using tile::GemmArgs;
+using tile::MmaTraits;
+
+__device__ __align__(16) uint32_t g_zero_page[4] = {0u, 0u, 0u, 0u};
+
+constexpr int kMaxSpatial = 6;
+
+// ------------------------------------------------------------------ implicit-GEMM A operand
+template <int NS>
+struct ConvSrc {
+    struct Geom {
+        FastDiv odim[NS];        // output spatial extents, outermost first
+        uint32_t idim[NS];       // input spatial extents
+        int32_t stride[NS], dil[NS], pad[NS];
+        FastDiv kdim[NS];        // kernel spatial extents
+        uint32_t xs[NS];         // Xp element stride of each spatial axis
+        uint32_t xn;             // Xp element stride of N
+        FastDiv cpairs;          // K pairs per kernel position (Cgp / pair elements)
+        uint32_t on, os[NS];     // output element strides: N, spatial axes
+    };
+    static constexpr bool kStrided = false;
+    // Per DMA instruction: the row's image offset (n, o * stride, and the lane's chunk folded
+    // in) and its strided spatial position packed 16 bits per axis.
+    struct AState { int32_t base[tile::DMA_A]; uint32_t pos[tile::DMA_A]; };
+
+    __device__ __forceinline__ static void decompose(const Geom& geo, uint32_t m, uint32_t (&o)[NS], uint32_t& n) {
+#pragma unroll
+        for (int d = NS - 1; d >= 0; --d) {
+            const uint32_t q = geo.odim[d].div(m);
+            o[d] = m - q * geo.odim[d].d;
+            m = q;
+        }
+        n = m;
+    }
+
+    template <typename S>
+    __device__ __forceinline__ static AState a_init(const GemmArgs& g, const Geom& geo, uint32_t m0, uint32_t rows_a,
+                                                    int wave, int lane) {
+        constexpr int CE = 16 / sizeof(S);
+        AState st;
+#pragma unroll
+        for (int i = 0; i < tile::DMA_A; i++) {
+            const int r = tile::dma_row(wave, i, tile::DMA_A, lane);
+            const uint32_t m = m0 + min((uint32_t)r, rows_a - 1);
+            uint32_t o[NS], n;
+            decompose(geo, m, o, n);
+            int32_t base = (int32_t)(n * geo.xn) + tile::dma_chunk(r, lane) * CE;
+            uint32_t pos = 0;
+#pragma unroll
+            for (int d = 0; d < NS; d++) {
+                const uint32_t p = o[d] * (uint32_t)geo.stride[d];
+                base += (int32_t)(p * geo.xs[d]);
+                pos |= p << (16 * d);
+            }
+            st.base[i] = base;
+            st.pos[i] = pos;
+        }
+        return st;
+    }
+
+    template <typename S>
+    __device__ __forceinline__ static void a_dma(char* lds, const S* Abat, const AState& st, const GemmArgs& g,
+                                                 const Geom& geo, uint32_t m0, uint32_t p, int wave, int lane) {
+        constexpr int PE = tile::ROWB / sizeof(S);       // K elements per pair
+        // wave-uniform: kernel position and channel block of pair p
+        uint32_t kpos = geo.cpairs.div(p);
+        const uint32_t cp = p - kpos * geo.cpairs.d;
+        int32_t kk[NS];
+        int32_t uoff = (int32_t)(cp * PE);
+#pragma unroll
+        for (int d = NS - 1; d >= 0; --d) {
+            const uint32_t q = geo.kdim[d].div(kpos);
+            const uint32_t k = kpos - q * geo.kdim[d].d;
+            kpos = q;
+            kk[d] = (int32_t)k * geo.dil[d] - geo.pad[d];
+            uoff += kk[d] * (int32_t)geo.xs[d];
+        }
+#pragma unroll
+        for (int i = 0; i < tile::DMA_A; i++) {
+            bool valid = true;
+#pragma unroll
+            for (int d = 0; d < NS; d++) {
+                const int32_t s = (int32_t)((st.pos[i] >> (16 * d)) & 0xffffu) + kk[d];
+                valid = valid && (uint32_t)s < geo.idim[d];
+            }
+            const S* src = Abat + (st.base[i] + uoff);
+            tile::dma16(valid ? (const void*)src : (const void*)g_zero_page, lds + (wave * tile::DMA_A + i) * 1024);
+        }
+    }
+
+    __device__ __forceinline__ static uint64_t row_off(const GemmArgs& g, const Geom& geo, uint32_t row) {
+        uint32_t o[NS], n;
+        decompose(geo, row, o, n);
+        uint64_t off = (uint64_t)n * geo.on;
+#pragma unroll
+        for (int d = 0; d < NS; d++) off += (uint64_t)o[d] * geo.os[d];
+        return off;
+    }
+    template <typename S>
+    __device__ __forceinline__ static bool row_vec_ok(const GemmArgs& g, const Geom& geo) {
+        bool ok = ((uint64_t)geo.on * sizeof(S)) % 16 == 0;
+#pragma unroll
+        for (int d = 0; d < NS; d++) ok = ok && ((uint64_t)geo.os[d] * sizeof(S)) % 16 == 0;
+        return ok;
+    }
+};
+
+// ------------------------------------------------------------------ packing
+struct ConvShape {
+    int ns;
+    uint32_t N, C, O, groups, Cg, Og;
+    uint32_t S[kMaxSpatial], K[kMaxSpatial], OS[kMaxSpatial];
+    uint64_t in_s[kMaxSpatial + 2], k_s[kMaxSpatial + 2], out_s[kMaxSpatial + 2];
+};
+
+// Xp[n, s.., g, c] = c < Cg ? in[n, s.., g Cg + c] : 0, one element per thread.
+struct PackInDesc {
+    int ns;
+    FastDiv dims[kMaxSpatial + 2];       // N, S.., groups * Cgp  (outermost first)
+    FastDiv cgp;
+    uint32_t Cg;
+    uint64_t s[kMaxSpatial + 2];         // input strides: N, spatial axes, channel
+};
+
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input_kernel(S* __restrict__ xp, const S* __restrict__ in, uint64_t total,
+                                                         PackInDesc d) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+        uint64_t rem = t;
+        const uint64_t gc = rem % d.dims[d.ns + 1].d;
+        rem /= d.dims[d.ns + 1].d;
+        uint64_t off = 0;
+        for (int a = d.ns; a >= 1; --a) {
+            off += (rem % d.dims[a].d) * d.s[a];
+            rem /= d.dims[a].d;
+        }
+        off += rem * d.s[0];
+        const uint32_t g = d.cgp.div((uint32_t)gc);
+        const uint32_t c = (uint32_t)gc - g * d.cgp.d;
+        xp[t] = c < d.Cg ? in[off + (uint64_t)(g * d.Cg + c) * d.s[d.ns + 1]] : S(0);
+    }
+}
+
+// Channel-major image (the spatial axes form one unit-stride run P, channels at stride sC, as an
+// NCHW tensor viewed NHWC): Xp[n, p, c] = in[n, c, p] as a tiled transpose through LDS, 64 x 64
+// per block, reads and writes both along their contiguous axis.  groups == 1 here.
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input_transpose_kernel(S* __restrict__ xp, const S* __restrict__ in,
+                                                                   uint32_t P, uint32_t C, uint32_t Cgp, uint64_t sN,
+                                                                   uint64_t sC) {
+    __shared__ S t[64][65];
+    const uint32_t p0 = blockIdx.x * 64, c0 = blockIdx.y * 64, n = blockIdx.z;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const S* src = in + (uint64_t)n * sN;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {                  // read: 64 channels x 64 positions
+        const uint32_t c = c0 + ty + 4 * i, p = p0 + tx;
+        t[ty + 4 * i][tx] = (c < C && p < P) ? src[(uint64_t)c * sC + p] : S(0);
+    }
+    __syncthreads();
+    S* dst = xp + (uint64_t)n * P * Cgp;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {                  // write: 64 positions x 64 channels
+        const uint32_t p = p0 + ty + 4 * i, c = c0 + tx;
+        if (p < P && c < Cgp) dst[(uint64_t)p * Cgp + c] = t[tx][ty + 4 * i];
+    }
+}
+
+// Wp[o, k.., c] = c < Cg ? kern[o, (flip ? K - 1 - k : k).., c] : 0.
+struct PackKDesc {
+    int ns;
+    FastDiv dims[kMaxSpatial + 2];       // O, K.., Cgp
+    uint32_t K[kMaxSpatial];
+    uint32_t Cg;
+    int flip;
+    uint64_t s[kMaxSpatial + 2];
+};
+
+template <typename S>
+__global__ __launch_bounds__(256) void pack_kernel_kernel(S* __restrict__ wp, const S* __restrict__ kern,
+                                                          uint64_t total, PackKDesc d) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+        uint64_t rem = t;
+        const uint32_t c = (uint32_t)(rem % d.dims[d.ns + 1].d);
+        rem /= d.dims[d.ns + 1].d;
+        uint64_t off = (uint64_t)c * d.s[d.ns + 1];
+        for (int a = d.ns; a >= 1; --a) {
+            const uint32_t k = (uint32_t)(rem % d.dims[a].d);
+            rem /= d.dims[a].d;
+            off += (uint64_t)(d.flip ? d.K[a - 1] - 1 - k : k) * d.s[a];
+        }
+        off += rem * d.s[0];
+        wp[t] = c < d.Cg ? kern[off] : S(0);
+    }
+}
+
+// ------------------------------------------------------------------ direct kernel
+struct DirectDesc {
+    int ns;
+    uint32_t N, O, Cg, Og, groups;
+    uint32_t S[kMaxSpatial], K[kMaxSpatial], OS[kMaxSpatial];
+    int32_t pad[kMaxSpatial], stride[kMaxSpatial], dil[kMaxSpatial], dil_lhs[kMaxSpatial];
+    uint64_t in_s[kMaxSpatial + 2], k_s[kMaxSpatial + 2], out_s[kMaxSpatial + 2];
+    int flip;
+    uint64_t kdot;                       // prod K * Cg
+};
+
+template <int DT>
+__global__ __launch_bounds__(256) void conv_direct_kernel(typename dt_traits<DT>::S* __restrict__ out,
+                                                          const typename dt_traits<DT>::S* __restrict__ in,
+                                                          const typename dt_traits<DT>::S* __restrict__ kern,
+                                                          uint64_t total, DirectDesc d) {
+    using Tr = dt_traits<DT>;
+    using S = typename Tr::S;
+    const uint64_t gstride = (uint64_t)gridDim.x * 256;
+    for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += gstride) {
+        // t -> (n, o_1 .. o_ns, oc), oc fastest
+        uint64_t rem = t;
+        const uint32_t oc = (uint32_t)(rem % d.O);
+        rem /= d.O;
+        int64_t base[kMaxSpatial];
+        uint64_t out_off = (uint64_t)oc * d.out_s[d.ns + 1];
+        for (int a = d.ns - 1; a >= 0; --a) {
+            const uint32_t o = (uint32_t)(rem % d.OS[a]);
+            rem /= d.OS[a];
+            base[a] = (int64_t)o * d.stride[a] - d.pad[a];
+            out_off += (uint64_t)o * d.out_s[a + 1];
+        }
+        const uint64_t n = rem;
+        out_off += n * d.out_s[0];
+        const uint32_t c0 = (oc / d.Og) * d.Cg;
+        using Acc = std::conditional_t<Tr::is_float, float, uint64_t>;
+        Acc acc = 0;
+        for (uint64_t tt = 0; tt < d.kdot; tt++) {
+            const uint32_t c = (uint32_t)(tt % d.Cg);
+            uint64_t rk = tt / d.Cg;
+            uint64_t ioff = n * d.in_s[0] + (uint64_t)(c0 + c) * d.in_s[d.ns + 1];
+            uint64_t koff = (uint64_t)oc * d.k_s[0] + (uint64_t)c * d.k_s[d.ns + 1];
+            bool valid = true;
+            for (int j = d.ns - 1; j >= 0; --j) {
+                const int64_t kj = (int64_t)(rk % d.K[j]);
+                rk /= d.K[j];
+                const int64_t s = base[j] + kj * d.dil[j];
+                const int64_t len = ((int64_t)d.S[j] - 1) * d.dil_lhs[j] + 1;
+                if (s < 0 || s >= len || (s % d.dil_lhs[j]) != 0) { valid = false; break; }
+                const int64_t kr = d.flip ? ((int64_t)d.K[j] - 1 - kj) : kj;
+                koff += (uint64_t)kr * d.k_s[j + 1];
+                ioff += (uint64_t)(s / d.dil_lhs[j]) * d.in_s[j + 1];
+            }
+            if (!valid) continue;
+            if constexpr (Tr::is_float) {
+                acc = __builtin_fmaf(Tr::ld(kern[koff]), Tr::ld(in[ioff]), acc);
+            } else {
+                acc += (uint64_t)(int64_t)kern[koff] * (uint64_t)(int64_t)in[ioff];
+            }
+        }
+        if constexpr (Tr::is_float) out[out_off] = Tr::st(acc);
+        else out[out_off] = (S)acc;
+    }
+}
+
+// ------------------------------------------------------------------ planning
+struct Plan {
+    bool mfma = false;
+    bool pack_in = false, pack_k = false;
+    uint32_t Cgp = 0;
+    size_t xp_bytes = 0, wp_bytes = 0;
+};
+
+inline size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+bool contiguous_channels_last(int ns, const uint32_t* shape, const uint64_t* s) {
+    uint64_t want = 1;
+    for (int a = ns + 1; a >= 0; --a) {
+        if (shape[a] != 1 && s[a] != want) return false;
+        want *= shape[a];
+    }
+    return true;
+}
+
+// The MFMA plan as far as the shapes and strides decide it (flip, dilations and pointer
+// alignment are checked again at launch).
+Plan plan_conv(int dtype, const ConvShape& cs) {
+    Plan p;
+    if (!(dtype == MX_FLOAT32 || dtype == MX_FLOAT16 || dtype == MX_BFLOAT16)) return p;
+    if (cs.ns < 1 || cs.ns > 2) return p;
+    const size_t es = dtype_size(dtype);
+    const uint32_t PE = (uint32_t)(tile::ROWB / es);
+    p.Cgp = (cs.Cg + PE - 1) / PE * PE;
+    uint64_t sp = 1, kp = 1, osp = 1;
+    for (int d = 0; d < cs.ns; d++) {
+        sp *= cs.S[d];
+        kp *= cs.K[d];
+        osp *= cs.OS[d];
+        if (cs.S[d] >= 32768 || (uint64_t)cs.OS[d] * 1 >= 32768) return p;
+    }
+    const uint64_t xp_elems = (uint64_t)cs.N * sp * cs.groups * p.Cgp;
+    const uint64_t K = kp * p.Cgp;
+    const uint64_t M = (uint64_t)cs.N * osp;
+    if (xp_elems >= (1ull << 31) || K >= (1ull << 31) || M >= (1ull << 32) || K * es * 256 >= (1ull << 32))
+        return p;
+    uint32_t ishape[kMaxSpatial + 2], kshape[kMaxSpatial + 2];
+    ishape[0] = cs.N;
+    kshape[0] = cs.O;
+    for (int d = 0; d < cs.ns; d++) { ishape[d + 1] = cs.S[d]; kshape[d + 1] = cs.K[d]; }
+    ishape[cs.ns + 1] = cs.C;
+    kshape[cs.ns + 1] = cs.Cg;
+    p.pack_in = !(p.Cgp == cs.Cg && contiguous_channels_last(cs.ns, ishape, cs.in_s));
+    p.pack_k = !(p.Cgp == cs.Cg && contiguous_channels_last(cs.ns, kshape, cs.k_s));
+    p.xp_bytes = p.pack_in ? align256(xp_elems * es) : 0;
+    p.wp_bytes = align256((uint64_t)cs.O * K * es);      // flip is unknown here: always counted
+    p.mfma = true;
+    return p;
+}
+
+int read_shape(int dtype, int ns, const uint32_t* in_shape, const uint32_t* k_shape, const uint32_t* out_shape,
+               const uint32_t* in_strides, const uint32_t* k_strides, const uint32_t* out_strides, int groups,
+               ConvShape& cs, const char* who) {
+    if (ns < 1 || ns > kMaxSpatial)
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": nspatial " + std::to_string(ns) + " outside [1, 6]");
+    if (!in_shape || !k_shape || !out_shape || !in_strides || !k_strides || !out_strides)
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": null descriptor");
+    if (groups < 1) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": groups must be >= 1");
+    cs.ns = ns;
+    cs.N = in_shape[0];
+    cs.C = in_shape[ns + 1];
+    cs.O = k_shape[0];
+    cs.Cg = k_shape[ns + 1];
+    cs.groups = (uint32_t)groups;
+    if (out_shape[0] != cs.N || out_shape[ns + 1] != cs.O)
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": output batch / channels do not match input / kernel");
+    if ((uint64_t)cs.Cg * cs.groups != cs.C || cs.O % cs.groups != 0)
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": channels do not divide into groups");
+    cs.Og = cs.O / cs.groups;
+    for (int d = 0; d < ns; d++) {
+        cs.S[d] = in_shape[d + 1];
+        cs.K[d] = k_shape[d + 1];
+        cs.OS[d] = out_shape[d + 1];
+    }
+    for (int a = 0; a < ns + 2; a++) {
+        cs.in_s[a] = in_strides[a];
+        cs.k_s[a] = k_strides[a];
+        cs.out_s[a] = out_strides[a];
+    }
+    (void)dtype;
+    return MX_OK;
+}
+
+template <typename S>
+int launch_pack_input(const ConvShape& cs, uint32_t Cgp, S* xp, const S* in, hipStream_t st) {
+    // channel-major special case: the spatial axes collapse into one unit-stride run
+    bool run = cs.groups == 1 && cs.in_s[cs.ns] == 1;
+    for (int d = cs.ns - 1; d >= 1 && run; --d) run = cs.in_s[d] == cs.in_s[d + 1] * cs.S[d];
+    uint64_t P = 1;
+    for (int d = 0; d < cs.ns; d++) P *= cs.S[d];
+    if (run && P < (1ull << 31) && cs.N < 65536) {
+        dim3 grid((uint32_t)((P + 63) / 64), (Cgp + 63) / 64, cs.N);
+        hipLaunchKernelGGL((pack_input_transpose_kernel<S>), grid, dim3(256), 0, st, xp, in, (uint32_t)P, cs.C, Cgp,
+                           cs.in_s[0], cs.in_s[cs.ns + 1]);
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    }
+    PackInDesc d{};
+    d.ns = cs.ns;
+    d.dims[0] = FastDiv(cs.N);
+    for (int a = 0; a < cs.ns; a++) d.dims[a + 1] = FastDiv(cs.S[a]);
+    d.dims[cs.ns + 1] = FastDiv(cs.groups * Cgp);
+    d.cgp = FastDiv(Cgp);
+    d.Cg = cs.Cg;
+    for (int a = 0; a < cs.ns + 2; a++) d.s[a] = cs.in_s[a];
+    const uint64_t total = (uint64_t)cs.N * P * cs.groups * Cgp;
+    const uint64_t want = (total + 255) / 256;
+    hipLaunchKernelGGL((pack_input_kernel<S>), dim3((uint32_t)(want < 65536 ? want : 65536)), dim3(256), 0, st, xp,
+                       in, total, d);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
+template <typename S>
+int launch_pack_kernel(const ConvShape& cs, uint32_t Cgp, int flip, S* wp, const S* kern, hipStream_t st) {
+    PackKDesc d{};
+    d.ns = cs.ns;
+    d.dims[0] = FastDiv(cs.O);
+    uint64_t total = (uint64_t)cs.O * Cgp;
+    for (int a = 0; a < cs.ns; a++) {
+        d.dims[a + 1] = FastDiv(cs.K[a]);
+        d.K[a] = cs.K[a];
+        total *= cs.K[a];
+    }
+    d.dims[cs.ns + 1] = FastDiv(Cgp);
+    d.Cg = cs.Cg;
+    d.flip = flip;
+    for (int a = 0; a < cs.ns + 2; a++) d.s[a] = cs.k_s[a];
+    const uint64_t want = (total + 255) / 256;
+    hipLaunchKernelGGL((pack_kernel_kernel<S>), dim3((uint32_t)(want < 65536 ? want : 65536)), dim3(256), 0, st, wp,
+                       kern, total, d);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
+template <int DT, int NS>
+int launch_implicit_gemm(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, const int* stride, const int* dil,
+                         void* out, const void* xp, const void* wp, hipStream_t st) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr uint32_t PE = tile::ROWB / sizeof(S);
+    typename ConvSrc<NS>::Geom geo{};
+    uint64_t M = cs.N, kpos = 1;
+    for (int d = 0; d < NS; d++) {
+        geo.odim[d] = FastDiv(cs.OS[d]);
+        geo.idim[d] = cs.S[d];
+        geo.stride[d] = stride[d];
+        geo.dil[d] = dil[d];
+        geo.pad[d] = pad_lo[d];
+        geo.kdim[d] = FastDiv(cs.K[d]);
+        M *= cs.OS[d];
+        kpos *= cs.K[d];
+    }
+    uint32_t xs = cs.groups * Cgp;
+    for (int d = NS - 1; d >= 0; --d) {
+        geo.xs[d] = xs;
+        xs *= cs.S[d];
+    }
+    geo.xn = xs;
+    geo.cpairs = FastDiv(Cgp / PE);
+    geo.on = (uint32_t)cs.out_s[0];
+    for (int d = 0; d < NS; d++) geo.os[d] = (uint32_t)cs.out_s[d + 1];
+
+    GemmArgs g{};
+    g.M = (uint32_t)M;
+    g.N = cs.Og;
+    g.K = (uint32_t)(kpos * Cgp);
+    g.lda = 0;
+    g.ka = 1;
+    g.ldb = g.K;
+    g.kb = 1;
+    g.ldc = 0;
+    g.cn = (uint32_t)cs.out_s[NS + 1];
+    g.batches = cs.groups;
+    if (cs.groups > 1) {
+        g.bd.n = 1;
+        g.bd.shape[0] = FastDiv(cs.groups);
+        g.bd.sA[0] = Cgp;
+        g.bd.sB[0] = cs.Og * g.K;
+        g.bd.sC[0] = (uint32_t)(cs.Og * cs.out_s[NS + 1]);
+    }
+    auto go = [&](auto bn) -> int {
+        constexpr int BN = decltype(bn)::value;
+        g.tiles_m = (g.M + tile::BM - 1) / tile::BM;
+        g.tiles_n = (g.N + BN - 1) / BN;
+        const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches;
+        if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: grid too large");
+        hipLaunchKernelGGL((tile::mfma_tile_kernel<DT, BN, true, ConvSrc<NS>>), dim3((uint32_t)blocks),
+                           dim3(tile::NTHREADS), 0, st, (S*)out, (const S*)xp, (const S*)wp, g, geo);
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    };
+    if (g.N <= 128) return go(std::integral_constant<int, 128>{});
+    return go(std::integral_constant<int, 256>{});
+}
+
+template <int DT>
+int launch_direct(const ConvShape& cs, const int* pad_lo, const int* stride, const int* dil, const int* dil_lhs,
+                  int flip, void* out, const void* in, const void* kern, hipStream_t st) {
+    using S = typename dt_traits<DT>::S;
+    DirectDesc d{};
+    d.ns = cs.ns;
+    d.N = cs.N; d.O = cs.O; d.Cg = cs.Cg; d.Og = cs.Og; d.groups = cs.groups;
+    uint64_t total = (uint64_t)cs.N * cs.O, kdot = cs.Cg;
+    for (int a = 0; a < cs.ns; a++) {
+        d.S[a] = cs.S[a]; d.K[a] = cs.K[a]; d.OS[a] = cs.OS[a];
+        d.pad[a] = pad_lo[a]; d.stride[a] = stride[a]; d.dil[a] = dil[a]; d.dil_lhs[a] = dil_lhs[a];
+        total *= cs.OS[a];
+        kdot *= cs.K[a];
+    }
+    for (int a = 0; a < cs.ns + 2; a++) { d.in_s[a] = cs.in_s[a]; d.k_s[a] = cs.k_s[a]; d.out_s[a] = cs.out_s[a]; }
+    d.flip = flip;
+    d.kdot = kdot;
+    if (total == 0) return MX_OK;
+    const uint64_t want = (total + 255) / 256;
+    hipLaunchKernelGGL((conv_direct_kernel<DT>), dim3((uint32_t)(want < 1048576 ? want : 1048576)), dim3(256), 0, st,
+                       (S*)out, (const S*)in, (const S*)kern, total, d);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
+template <int DT>
+int launch_mfma_path(const ConvShape& cs, const Plan& p, const int* pad_lo, const int* stride, const int* dil,
+                     int flip, void* out, const void* in, const void* kern, void* ws, hipStream_t st) {
+    using S = typename MmaTraits<DT>::S;
+    char* w = static_cast<char*>(ws);
+    const void* xp = in;
+    if (p.pack_in) {
+        int rc = launch_pack_input<S>(cs, p.Cgp, reinterpret_cast<S*>(w), static_cast<const S*>(in), st);
+        if (rc) return rc;
+        xp = w;
+        w += p.xp_bytes;
+    }
+    const void* wp = kern;
+    if (p.pack_k || flip) {
+        int rc = launch_pack_kernel<S>(cs, p.Cgp, flip, reinterpret_cast<S*>(w), static_cast<const S*>(kern), st);
+        if (rc) return rc;
+        wp = w;
+    }
+    if (cs.ns == 1) return launch_implicit_gemm<DT, 1>(cs, p.Cgp, pad_lo, stride, dil, out, xp, wp, st);
+    return launch_implicit_gemm<DT, 2>(cs, p.Cgp, pad_lo, stride, dil, out, xp, wp, st);
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_conv_workspace_bytes(int dtype, int nspatial, const uint32_t* in_shape, const uint32_t* k_shape,
+                                       const uint32_t* out_shape, const uint32_t* in_strides,
+                                       const uint32_t* k_strides, const uint32_t* out_strides, int groups,
+                                       size_t* bytes) {
+    if (!bytes) return fail(MX_ERR_INVALID_ARG, "mx_conv_workspace_bytes: null result pointer");
+    *bytes = 0;
+    ConvShape cs{};
+    int rc = read_shape(dtype, nspatial, in_shape, k_shape, out_shape, in_strides, k_strides, out_strides, groups, cs,
+                        "mx_conv_workspace_bytes");
+    if (rc) return rc;
+    const Plan p = plan_conv(dtype, cs);
+    if (p.mfma) *bytes = p.xp_bytes + p.wp_bytes;
+    return MX_OK;
+}
+
+extern "C" int mx_launch_conv_nd(int dtype, int nspatial, const uint32_t* in_shape, const uint32_t* k_shape,
+                                 const uint32_t* out_shape, const uint32_t* in_strides, const uint32_t* k_strides,
+                                 const uint32_t* out_strides, const int* pad_lo, const int* stride,
+                                 const int* dil_rhs, const int* dil_lhs, int groups, int flip, void* out,
+                                 const void* in, const void* kern, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+    ConvShape cs{};
+    int rc = read_shape(dtype, nspatial, in_shape, k_shape, out_shape, in_strides, k_strides, out_strides, groups, cs,
+                        "mx_launch_conv_nd");
+    if (rc) return rc;
+    if (!pad_lo || !stride || !dil_rhs || !dil_lhs) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: null geometry");
+    bool no_lhs_dil = true;
+    for (int d = 0; d < nspatial; d++) {
+        if (stride[d] < 1 || dil_rhs[d] < 1 || dil_lhs[d] < 1)
+            return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: stride and dilations must be >= 1");
+        no_lhs_dil = no_lhs_dil && dil_lhs[d] == 1;
+    }
+    uint64_t total = (uint64_t)cs.N * cs.O;
+    for (int d = 0; d < nspatial; d++) total *= cs.OS[d];
+    if (total == 0) return MX_OK;
+    if (!out || !in || !kern) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: null buffer");
+    hipStream_t st;
+    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+
+    const Plan p = plan_conv(dtype, cs);
+    bool spatial_ok = true;                           // strided positions fit the 16-bit packing
+    for (int d = 0; d < nspatial && p.mfma; d++)
+        spatial_ok = spatial_ok && (uint64_t)(cs.OS[d] ? cs.OS[d] - 1 : 0) * stride[d] < 32768 &&
+                     (uint64_t)pad_lo[d] < 32768 && (uint64_t)(cs.K[d] - 1) * dil_rhs[d] < 32768;
+    if (p.mfma && no_lhs_dil && spatial_ok) {
+        const size_t need = p.xp_bytes + p.wp_bytes;
+        const bool aligned = (p.pack_in || (uintptr_t)in % 16 == 0) && (p.pack_k || flip || (uintptr_t)kern % 16 == 0) &&
+                             ((uintptr_t)workspace % 16 == 0);
+        if (workspace_bytes < need || (!workspace && need))
+            return fail(MX_ERR_WORKSPACE, "mx_launch_conv_nd: workspace of " + std::to_string(need) +
+                                              " bytes required (mx_conv_workspace_bytes)");
+        if (aligned) {
+            switch (dtype) {
+            case MX_FLOAT32: return launch_mfma_path<MX_FLOAT32>(cs, p, pad_lo, stride, dil_rhs, flip, out, in, kern, workspace, st);
+            case MX_FLOAT16: return launch_mfma_path<MX_FLOAT16>(cs, p, pad_lo, stride, dil_rhs, flip, out, in, kern, workspace, st);
+            case MX_BFLOAT16: return launch_mfma_path<MX_BFLOAT16>(cs, p, pad_lo, stride, dil_rhs, flip, out, in, kern, workspace, st);
+            default: break;
+            }
+        }
+    }
+    switch (dtype) {
+    case MX_FLOAT32: return launch_direct<MX_FLOAT32>(cs, pad_lo, stride, dil_rhs, dil_lhs, flip, out, in, kern, st);
+    case MX_FLOAT16: return launch_direct<MX_FLOAT16>(cs, pad_lo, stride, dil_rhs, dil_lhs, flip, out, in, kern, st);
+    case MX_BFLOAT16: return launch_direct<MX_BFLOAT16>(cs, pad_lo, stride, dil_rhs, dil_lhs, flip, out, in, kern, st);
+    case MX_INT32: return launch_direct<MX_INT32>(cs, pad_lo, stride, dil_rhs, dil_lhs, flip, out, in, kern, st);
+    case MX_INT64: return launch_direct<MX_INT64>(cs, pad_lo, stride, dil_rhs, dil_lhs, flip, out, in, kern, st);
+    default:
+        return fail(MX_ERR_UNSUPPORTED, "mx_launch_conv_nd: no kernel for dtype " + std::to_string(dtype));
+    }
+}

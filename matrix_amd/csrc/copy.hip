@@ -1,0 +1,229 @@
+// copy.hip -- strided copy with dtype cast: dst[idx . sDst] = cast(src[idx . sSrc]).
+//
+// Replaces copyGPUinplace / copyGPUinplaceTypeCasted and the CopyInplaceGPU kernels
+// (Matrix.mm:1699-1976, Copy.metal:14-80); the element semantics are those of the CPU copy
+// (copyCPUinplace / copyCPUinplaceTypeCasted, matrix.h:1337-1550), whose dtype_cast
+// (matrix.h:306-313) is a static_cast:
+//   - float -> float goes through float (16-bit targets round to nearest even);
+//   - integer -> float rounds to nearest even (64-bit integers included);
+//   - float -> integer truncates toward zero and saturates (NaN -> 0): 8- and 16-bit targets
+//     saturate to the 32-bit range first and then keep the low bits, as arm64's fcvtzs /
+//     fcvtzu followed by a narrowing store do;
+//   - integer -> integer keeps the low bits (two's complement);
+//   - anything -> bool is (value != 0); bool reads as 0 / 1.
+//
+// Layout: the iteration space is a collapsed descriptor (any cdims <= 8).  Same-dtype copies
+// whose innermost axis is unit-stride on both sides move 16 bytes per thread; everything else
+// runs one element per thread with FastDiv index decomposition.
+#include "common.hpp"
+
+namespace mx {
+namespace {
+
+// A source element widened to one of three carriers, as the cast needs it.
+struct Wide {
+    int kind;            // 0 float, 1 signed integer, 2 unsigned integer
+    float f;
+    int64_t i;
+    uint64_t u;
+};
+
+template <int SD>
+__device__ __forceinline__ Wide widen(typename dt_traits<SD>::S x) {
+    Wide w{0, 0.0f, 0, 0};
+    if constexpr (dt_traits<SD>::is_float) {
+        w.kind = 0;
+        w.f = dt_traits<SD>::ld(x);
+    } else if constexpr (SD == MX_BOOL) {
+        w.kind = 2;
+        w.u = x != 0;
+    } else if constexpr (dt_traits<SD>::is_signed) {
+        w.kind = 1;
+        w.i = (int64_t)x;
+    } else {
+        w.kind = 2;
+        w.u = (uint64_t)x;
+    }
+    return w;
+}
+
+__device__ __forceinline__ int32_t sat_i32(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return INT32_MAX;
+    if (v <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)v;
+}
+__device__ __forceinline__ uint32_t sat_u32(float v) {
+    if (v != v || v <= 0.0f) return 0;
+    if (v >= 4294967296.0f) return UINT32_MAX;
+    return (uint32_t)v;
+}
+__device__ __forceinline__ int64_t sat_i64(float v) {
+    if (v != v) return 0;
+    if (v >= 9.2233720368547758e18f) return INT64_MAX;
+    if (v <= -9.2233720368547758e18f) return INT64_MIN;
+    return (int64_t)v;
+}
+__device__ __forceinline__ uint64_t sat_u64(float v) {
+    if (v != v || v <= 0.0f) return 0;
+    if (v >= 1.8446744073709552e19f) return UINT64_MAX;
+    return (uint64_t)v;
+}
+
+template <int DD>
+__device__ __forceinline__ typename dt_traits<DD>::S narrow(const Wide& w) {
+    using Tr = dt_traits<DD>;
+    using S = typename Tr::S;
+    if constexpr (Tr::is_float) {
+        const float v = w.kind == 0 ? w.f : (w.kind == 1 ? (float)w.i : (float)w.u);
+        return Tr::st(v);
+    } else if constexpr (DD == MX_BOOL) {
+        return (S)(w.kind == 0 ? (w.f != 0.0f) : ((w.kind == 1 ? (uint64_t)w.i : w.u) != 0));
+    } else {
+        const int64_t iv = w.kind == 1 ? w.i : (int64_t)w.u;       // integer sources
+        const uint64_t uv = (uint64_t)iv;
+        if constexpr (DD == MX_INT64) return w.kind == 0 ? sat_i64(w.f) : iv;
+        else if constexpr (DD == MX_UINT64) return w.kind == 0 ? sat_u64(w.f) : uv;
+        else if constexpr (Tr::is_signed) return w.kind == 0 ? (S)sat_i32(w.f) : (S)iv;
+        else return w.kind == 0 ? (S)sat_u32(w.f) : (S)uv;
+    }
+}
+
+struct CopyDesc {
+    int n;
+    FastDiv shape[MX_MAX_DIMS];
+    uint32_t sd[MX_MAX_DIMS], ss[MX_MAX_DIMS];
+};
+
+template <int DD, int SD>
+__global__ __launch_bounds__(256) void copy_scalar_kernel(typename dt_traits<DD>::S* __restrict__ dst,
+                                                          const typename dt_traits<SD>::S* __restrict__ src,
+                                                          uint64_t total, CopyDesc d) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t g = (uint64_t)blockIdx.x * 256 + threadIdx.x; g < total; g += stride) {
+        uint64_t od = 0, os = 0;
+        if (g < 0x100000000ull) {                // 32-bit decomposition (every shape axis < 2^32)
+            uint32_t rem = (uint32_t)g;
+            for (int k = d.n - 1; k >= 0; --k) {
+                const uint32_t q = d.shape[k].div(rem);
+                const uint32_t idx = rem - q * d.shape[k].d;
+                rem = q;
+                od += (uint64_t)idx * d.sd[k];
+                os += (uint64_t)idx * d.ss[k];
+            }
+        } else {
+            uint64_t rem = g;
+            for (int k = d.n - 1; k >= 0; --k) {
+                const uint64_t idx = rem % d.shape[k].d;
+                rem /= d.shape[k].d;
+                od += idx * d.sd[k];
+                os += idx * d.ss[k];
+            }
+        }
+        dst[od] = narrow<DD>(widen<SD>(src[os]));
+    }
+}
+
+// Same dtype, innermost axis contiguous on both sides and a multiple of the 16-byte vector:
+// each thread moves one 16-byte chunk; the outer axes decompose the chunk's row.
+struct RowDesc {
+    int n;                                  // outer axes
+    FastDiv shape[MX_MAX_DIMS];
+    uint32_t sd[MX_MAX_DIMS], ss[MX_MAX_DIMS];
+    FastDiv row_chunks;                     // 16-byte chunks per innermost row
+};
+
+__global__ __launch_bounds__(256) void copy_rows16_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                          uint64_t chunks, uint32_t elem_bytes, RowDesc d) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    for (uint64_t g = (uint64_t)blockIdx.x * 256 + threadIdx.x; g < chunks; g += stride) {
+        const uint32_t gg = (uint32_t)g;                 // launcher keeps chunks < 2^32
+        uint32_t row = d.row_chunks.div(gg);
+        const uint32_t c = gg - row * d.row_chunks.d;
+        uint64_t od = 0, os = 0;                          // element offsets of the row start
+        for (int k = d.n - 1; k >= 0; --k) {
+            const uint32_t q = d.shape[k].div(row);
+            const uint32_t idx = row - q * d.shape[k].d;
+            row = q;
+            od += (uint64_t)idx * d.sd[k];
+            os += (uint64_t)idx * d.ss[k];
+        }
+        const uint32_t per = 16 / elem_bytes;
+        dst[od / per + c] = src[os / per + c];
+    }
+}
+
+template <typename F>
+bool dispatch_pair(int dd, int sd, F&& f) {
+    bool ok = false;
+    dispatch_dtype(dd, [&](auto D) {
+        ok = dispatch_dtype(sd, [&](auto S) { f(D, S); });
+    });
+    return ok;
+}
+
+}  // namespace
+}  // namespace mx
+
+using namespace mx;
+
+extern "C" int mx_launch_copy_strided(int dst_dtype, int src_dtype, int cdims, const uint32_t* shape,
+                                      const uint32_t* sDst, const uint32_t* sSrc, void* dst, const void* src,
+                                      void* stream) {
+    if (cdims < 0 || cdims > MX_MAX_DIMS)
+        return fail(MX_ERR_INVALID_ARG, "mx_launch_copy_strided: cdims " + std::to_string(cdims) + " outside [0, 8]");
+    if (cdims > 0 && (!shape || !sDst || !sSrc)) return fail(MX_ERR_INVALID_ARG, "mx_launch_copy_strided: null descriptor");
+    if (dtype_size(dst_dtype) == 0 || dtype_size(src_dtype) == 0 || dst_dtype == MX_COMPLEX64 ||
+        src_dtype == MX_COMPLEX64)
+        return fail(MX_ERR_UNSUPPORTED, "mx_launch_copy_strided: no kernel for dtypes " + std::to_string(dst_dtype) +
+                                            " <- " + std::to_string(src_dtype));
+    uint64_t total = 1;
+    for (int k = 0; k < cdims; k++) total *= shape[k];
+    if (total == 0) return MX_OK;
+    if (!dst || !src) return fail(MX_ERR_INVALID_ARG, "mx_launch_copy_strided: null buffer");
+    hipStream_t st;
+    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+
+    const size_t es = dtype_size(dst_dtype);
+    // 16-byte row path
+    if (dst_dtype == src_dtype && cdims >= 1 && sDst[cdims - 1] == 1 && sSrc[cdims - 1] == 1 &&
+        (shape[cdims - 1] * es) % 16 == 0 && (uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0) {
+        const uint32_t per = (uint32_t)(16 / es);
+        bool aligned = true;
+        RowDesc d{};
+        d.n = cdims - 1;
+        for (int k = 0; k < cdims - 1; k++) {
+            d.shape[k] = FastDiv(shape[k]);
+            d.sd[k] = sDst[k];
+            d.ss[k] = sSrc[k];
+            if (sDst[k] % per || sSrc[k] % per) aligned = false;
+        }
+        const uint64_t chunks = total / per;
+        if (aligned && chunks < 0xffffffffull) {
+            d.row_chunks = FastDiv(shape[cdims - 1] / per);
+            const uint64_t want = (chunks + 255) / 256;
+            const uint32_t blocks = (uint32_t)(want < 65536 ? want : 65536);
+            hipLaunchKernelGGL(copy_rows16_kernel, dim3(blocks), dim3(256), 0, st, (uint4*)dst, (const uint4*)src,
+                               chunks, (uint32_t)es, d);
+            MX_HIP(hipGetLastError());
+            return MX_OK;
+        }
+    }
+    CopyDesc d{};
+    d.n = cdims;
+    for (int k = 0; k < cdims; k++) {
+        d.shape[k] = FastDiv(shape[k]);
+        d.sd[k] = sDst[k];
+        d.ss[k] = sSrc[k];
+    }
+    const uint64_t want = (total + 255) / 256;
+    const uint32_t blocks = (uint32_t)(want < 65536 ? want : 65536);
+    int rc = MX_OK;
+    dispatch_pair(dst_dtype, src_dtype, [&](auto D, auto S) {
+        constexpr int DD = decltype(D)::value, SD = decltype(S)::value;
+        hipLaunchKernelGGL((copy_scalar_kernel<DD, SD>), dim3(blocks), dim3(256), 0, st,
+                           (typename dt_traits<DD>::S*)dst, (const typename dt_traits<SD>::S*)src, total, d);
+        if (hipGetLastError() != hipSuccess) rc = fail(MX_ERR_HIP, "mx_launch_copy_strided: launch failed");
+    });
+    return rc;
+}

@@ -1,0 +1,534 @@
+// mfma_tile.hpp -- the CDNA4 matrix-core tile kernel shared by batched MatMul (gemm.hip) and
+// ConvolutionND as an implicit GEMM (conv.hip).
+//
+// C[b, m, n] = sum_k A[b, m, k] * Bt[b, n, k], both operands K-major (the layout the reference
+// hands its backends: dot() packs B^T, Matrix.mm:7074-7089; the conv kernel is OHWI,
+// Matrix.mm:12274-12277).  float16 / bfloat16: v_mfma_f32_32x32x16_{f16,bf16}, fp32
+// accumulation, one rounding on store.  float32: v_mfma_f32_32x32x2_f32.
+//
+// Tiling: a 256-thread block computes a 256 x BN tile of C (BN = 256 or 128) as 2 x 2 waves of
+// 128 x BN/2 (4 x BN/64 MFMA tiles of 32 x 32 per wave, fp32 accumulators in AGPRs).  A K step
+// covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
+// K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
+// (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
+// global_load_lds_dwordx4) fill the slot of pair p + 2 while pair p + 1 is consumed; fragments
+// are double-buffered in registers, and the workgroup meets one barrier per pair.  Each slot is
+// its own __shared__ array, so the compiler can tell the DMA into one slot from the reads of the
+// other and adds no waits of its own.  LDS rows are 8 chunks of 16 bytes, swizzled so that one
+// MFMA operand read is bank-conflict free.  Block ids are remapped so that the tiles one XCD
+// (one L2) runs are consecutive M panels with all their N tiles.
+//
+// Where the A rows come from is a policy (Src): a strided matrix (GEMM) or an on-the-fly
+// im2col gather from a channels-last image (implicit-GEMM convolution), whose out-of-image
+// taps read a zero page.  The same policy maps a C row to its output offset.
+#pragma once
+#include "common.hpp"
+
+namespace mx {
+namespace tile {
+
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef __bf16 b8v __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256;
+constexpr int STEPB = 64;                 // bytes of K per row in one K step (one MFMA round)
+constexpr int ROWB = 2 * STEPB;           // bytes of one LDS row: a K pair, one 128-byte line
+constexpr int CPR = ROWB / 16;            // 16-byte chunks per LDS row
+constexpr int STEP_CHUNKS = STEPB / 16;
+constexpr int NTHREADS = 256;
+constexpr int NUM_XCD = 8;
+constexpr int DMA_A = BM * ROWB / 1024 / 4;            // 1 KB DMA instructions per wave, A slot
+template <int BN> constexpr int kDmaB = BN * ROWB / 1024 / 4;
+
+template <int DT> struct MmaTraits;
+template <> struct MmaTraits<MX_FLOAT16> { using S = uint16_t; };
+template <> struct MmaTraits<MX_BFLOAT16> { using S = uint16_t; };
+template <> struct MmaTraits<MX_FLOAT32> { using S = float; };
+
+struct BatchDesc {                // batch axes (all but the last two of a collapsed descriptor)
+    int n;
+    FastDiv shape[MX_MAX_DIMS];
+    uint32_t sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sC[MX_MAX_DIMS];
+};
+
+struct GemmArgs {
+    uint32_t M, N, K;
+    uint32_t lda, ldb;            // row strides (elements) of A [M, K] and Bt [N, K]
+    uint32_t ka, kb;              // K strides of A and Bt (1 on the DMA path)
+    uint32_t ldc, cn;             // C strides: row (M) and column (N)
+    uint32_t tiles_m, tiles_n, batches;
+    BatchDesc bd;
+};
+
+// LDS swizzle: logical chunk c of row r is stored at c ^ ((r >> 1) & 7).  The LDS serves a
+// 128-bit read 16 lanes (256 bytes, 64 banks) at a time; one MFMA operand read has 16 lanes on
+// 16 consecutive rows with the same logical chunk, whose 16-byte bank groups
+// 8 (r % 2) + stored chunk are then all distinct.
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+// Block id -> (batch, tile_m, tile_n).  Hardware dispatch hands block i to XCD i % 8; the
+// remap gives each XCD a contiguous run of logical tiles, ordered M panel by M panel.
+__device__ __forceinline__ void tile_of(uint32_t id, uint32_t nblocks, uint32_t tiles_m, uint32_t tiles_n,
+                                        uint32_t& b, uint32_t& tm, uint32_t& tn) {
+    const uint32_t per = nblocks / NUM_XCD, rem = nblocks % NUM_XCD;
+    const uint32_t x = id % NUM_XCD, j = id / NUM_XCD;
+    const uint32_t logical = (x < rem) ? x * (per + 1) + j : rem * (per + 1) + (x - rem) * per + j;
+    const uint32_t tiles = tiles_m * tiles_n;
+    b = logical / tiles;
+    const uint32_t t = logical - b * tiles;
+    tm = t / tiles_n;
+    tn = t - tm * tiles_n;
+}
+
+// K tail or strided operands: one K step (the first half of an LDS row) of a ROWS-row tile
+// through registers, element loads, zero past K (zeros keep the tail exact).  This thread's
+// chunk q = tid + 256 i is row q / 4, logical chunk q % 4.  Rows past the operand's end re-read
+// its last row (their products land only in C rows / columns that are never stored).
+template <int ROWS> constexpr int kTailChunks = ROWS * STEP_CHUNKS / NTHREADS;
+
+template <typename S, int ROWS>
+__device__ __forceinline__ void load_tile_guarded(uint4 (&r)[kTailChunks<ROWS>], const S* __restrict__ base,
+                                                  uint32_t rows_valid, uint32_t ld, uint32_t kstride, uint32_t k0,
+                                                  uint32_t K) {
+    constexpr int CE = 16 / sizeof(S);
+#pragma unroll
+    for (int i = 0; i < kTailChunks<ROWS>; i++) {
+        const int q = threadIdx.x + NTHREADS * i;
+        const uint32_t row = min((uint32_t)(q / STEP_CHUNKS), rows_valid - 1);
+        const uint32_t k = k0 + (q % STEP_CHUNKS) * CE;
+        S tmp[CE];
+#pragma unroll
+        for (int e = 0; e < CE; e++)
+            tmp[e] = (k + e < K) ? base[(uint64_t)row * ld + (uint64_t)(k + e) * kstride] : S(0);
+        __builtin_memcpy(&r[i], tmp, 16);
+    }
+}
+
+template <int ROWS>
+__device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[kTailChunks<ROWS>]) {
+#pragma unroll
+    for (int i = 0; i < kTailChunks<ROWS>; i++) {
+        const int q = threadIdx.x + NTHREADS * i;
+        const int row = q / STEP_CHUNKS, c = q % STEP_CHUNKS;
+        *reinterpret_cast<uint4*>(lds + row * ROWB + swz(row, c) * 16) = r[i];
+    }
+}
+
+// One K step's operand fragments for one wave (4 A tiles, WNT Bt tiles of 32 rows).  The step
+// is half HALF of the LDS rows (logical chunks 4 HALF .. 4 HALF + 3).  16-bit types: a K block
+// is 16 elements = 2 chunks; lane half h holds chunk 2 kb + h of the step.  fp32: the step is
+// one K block of 16 elements = 4 chunks; lane half h holds chunks 2h, 2h + 1 (K offsets
+// 8h .. 8h + 7); MFMA substep s consumes element s, so the two lane halves supply k = s and
+// k = 8 + s.
+template <int DT, int WNT> struct Frags;
+template <int WNT> struct Frags<MX_FLOAT16, WNT> { static constexpr int KB = 2; h8v a[KB][4], b[KB][WNT]; };
+template <int WNT> struct Frags<MX_BFLOAT16, WNT> { static constexpr int KB = 2; b8v a[KB][4], b[KB][WNT]; };
+template <int WNT> struct Frags<MX_FLOAT32, WNT> { static constexpr int KB = 1; float4 a[KB][4][2], b[KB][WNT][2]; };
+
+template <int DT, int WNT, int HALF>
+__device__ __forceinline__ void read_frags(Frags<DT, WNT>& f, const char* la, const char* lb, int wm, int wn,
+                                           int lane) {
+    const int r32 = lane & 31, h = lane >> 5;
+    constexpr int C0 = HALF * STEP_CHUNKS;
+#pragma unroll
+    for (int kb = 0; kb < Frags<DT, WNT>::KB; kb++) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int ra = wm * 128 + t * 32 + r32;
+            if constexpr (DT == MX_FLOAT32) {
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+                    f.a[kb][t][u] = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, C0 + 2 * h + u) * 16);
+            } else {
+                using V = std::remove_reference_t<decltype(f.a[0][0])>;
+                f.a[kb][t] = *reinterpret_cast<const V*>(la + ra * ROWB + swz(ra, C0 + 2 * kb + h) * 16);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int rb = wn * (WNT * 32) + t * 32 + r32;
+            if constexpr (DT == MX_FLOAT32) {
+#pragma unroll
+                for (int u = 0; u < 2; u++)
+                    f.b[kb][t][u] = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, C0 + 2 * h + u) * 16);
+            } else {
+                using V = std::remove_reference_t<decltype(f.b[0][0])>;
+                f.b[kb][t] = *reinterpret_cast<const V*>(lb + rb * ROWB + swz(rb, C0 + 2 * kb + h) * 16);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float f4_at(const float4 (&v)[2], int s) {
+    const float4& q = v[s >> 2];
+    switch (s & 3) { case 0: return q.x; case 1: return q.y; case 2: return q.z; default: return q.w; }
+}
+
+// MFMAs of the step for A tile rows I0 .. I1 - 1 of the wave's 4 x WNT grid.  The Bt fragment
+// goes in the MFMA's first operand slot and the A fragment in the second, so the 32 x 32 result
+// is the C^T tile: lane l holds C row (l % 32) and, in acc[4 q .. 4 q + 3], the 4 consecutive C
+// columns 8 q + 4 (l / 32) .. + 3 -- one vector store per (q) in the epilogue.
+template <int DT, int WNT, int I0 = 0, int I1 = 4>
+__device__ __forceinline__ void mma_step(f16v (&acc)[4][WNT], const Frags<DT, WNT>& f) {
+#pragma unroll
+    for (int kb = 0; kb < Frags<DT, WNT>::KB; kb++) {
+        if constexpr (DT == MX_FLOAT32) {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int i = I0; i < I1; i++)
+#pragma unroll
+                    for (int j = 0; j < WNT; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_at(f.b[kb][j], s), f4_at(f.a[kb][i], s),
+                                                                        acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = I0; i < I1; i++)
+#pragma unroll
+                for (int j = 0; j < WNT; j++) {
+                    if constexpr (DT == MX_FLOAT16)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.b[kb][j], f.a[kb][i], acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[kb][j], f.a[kb][i], acc[i][j], 0, 0, 0);
+                }
+        }
+    }
+}
+
+// Direct global -> LDS copy of one operand's K pair (two steps, 128 bytes of each row -- whole
+// L2 lines).  Each of a wave's DMA instructions fills 1 KB = 8 LDS rows; lane L lands at row
+// r = 8 p + L / 8, stored chunk L % 8, so it fetches the logical chunk that swz() stores there
+// (swz is its own inverse).  For a strided matrix the lane's byte offsets from the tile's first
+// row are fixed for the whole K loop; each pair adds its K offset to the wave-uniform base.
+// The offsets are 32-bit: the launcher keeps the tile's rows below 4 GiB.
+template <int N> struct DmaOffsets { uint32_t v[N]; };
+
+__device__ __forceinline__ int dma_row(int wave, int i, int per_wave, int lane) {
+    return (wave * per_wave + i) * 8 + lane / CPR;
+}
+__device__ __forceinline__ int dma_chunk(int row, int lane) { return swz(row, lane % CPR); }
+
+template <typename S, int N>
+__device__ __forceinline__ DmaOffsets<N> dma_offsets(uint32_t rows_valid, uint32_t ld, int wave, int lane) {
+    constexpr int CE = 16 / sizeof(S);
+    DmaOffsets<N> o;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int r = dma_row(wave, i, N, lane);
+        const uint32_t row = min((uint32_t)r, rows_valid - 1);
+        o.v[i] = (row * ld + dma_chunk(r, lane) * CE) * (uint32_t)sizeof(S);
+    }
+    return o;
+}
+
+__device__ __forceinline__ void dma16(const void* src, char* lds_chunk_base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_chunk_base, 16, 0, 0);
+}
+
+template <typename S, int N>
+__device__ __forceinline__ void dma_rows(char* lds, const S* __restrict__ base, const DmaOffsets<N>& o, uint32_t k0,
+                                         int wave) {
+    const char* kbase = reinterpret_cast<const char*>(base + k0);
+#pragma unroll
+    for (int i = 0; i < N; i++) dma16(kbase + o.v[i], lds + (wave * N + i) * 1024);
+}
+
+// s_waitcnt vmcnt(N), expcnt / lgkmcnt left at their maximum (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Instruction order within a K step, so the LDS and the memory pipeline work under the matrix
+// core instead of before it (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read, 0x020
+// vector-memory read).  A slot is one MFMA for 16-bit types and four for fp32; a step has
+// 8 WNT slots, 2 (4 + WNT) fragment reads, and a pair DMA_A + kDmaB instructions per wave.
+// The fragment reads go out early in their window so that they have returned (LDS latency is
+// several MFMAs) before the next step's first MFMA needs them.
+template <int DT> constexpr int kMfmaPerSlot = DT == MX_FLOAT32 ? 4 : 1;
+
+// First step of a pair: the next step's fragment reads, one per leading MFMA slot.
+template <int DT, int WNT>
+__device__ __forceinline__ void interleave_even() {
+    constexpr int MF = kMfmaPerSlot<DT>, SLOTS = 8 * WNT, NR = 2 * (4 + WNT);
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, (SLOTS - NR) * MF, 0);
+}
+
+// Second step of a pair, after its barrier (4 WNT slots left): the next step's fragment reads
+// over the first half of the slots, the DMA of the pair two ahead over all of them.
+template <int DT, int WNT, int BN>
+__device__ __forceinline__ void interleave_odd() {
+    constexpr int MF = kMfmaPerSlot<DT>, H = 4 * WNT, NR = 2 * (4 + WNT), ND = DMA_A + kDmaB<BN>;
+    constexpr int RPS = NR / (H / 2);                          // reads per slot, first half
+    constexpr int D1 = (ND + H - 1) / H;                       // DMAs per slot, first half
+    constexpr int D2 = (ND - D1 * (H / 2)) / (H / 2);          // DMAs per slot, second half
+    static_assert(RPS * (H / 2) == NR && D1 * (H / 2) + D2 * (H / 2) == ND, "interleave counts");
+#pragma unroll
+    for (int i = 0; i < H / 2; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, RPS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, D1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < H / 2; i++) {
+        if constexpr (D2 > 0) __builtin_amdgcn_sched_group_barrier(0x020, D2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+    }
+}
+
+// Workgroup barrier for the DMA ring.  __syncthreads() carries a workgroup release fence that
+// waits for every outstanding vector-memory operation.  The ring orders its LDS traffic itself:
+// each wave waits (vmcnt) for its DMA of the pair it is about to read, and a slot is refilled
+// only after the barrier that follows every wave's reads of it (lgkmcnt(0): this wave's reads
+// have returned).  The wait is the compiler's own s_waitcnt (lgkmcnt(0); vmcnt / expcnt at their
+// maximum), so its wait bookkeeping knows every fragment read has returned; s_barrier needs no
+// implicit wait on gfx950 (back-off barrier), and the empty asm statements keep LDS accesses from
+// moving across.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// ------------------------------------------------------------------ the tile kernel
+// Src provides:
+//   Geom                                  extra kernel argument (empty for GEMM)
+//   static constexpr bool kStrided        A may take the guarded K-tail path
+//   AState a_init<S>(g, geo, m0, wave, lane)          per-lane A addressing state
+//   void a_dma<S>(lds, A, st, g, geo, m0, pair, wave, lane)   one pair of the A slot
+//   uint64_t row_off(g, geo, row)         element offset of C row `row` (batch offset apart)
+//   bool row_vec_ok<S>(g, geo)            every row offset is a multiple of 16 bytes
+template <int DT, int BN, bool VEC, class Src>
+__global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<DT>::S* __restrict__ C,
+                                                             const typename MmaTraits<DT>::S* __restrict__ A,
+                                                             const typename MmaTraits<DT>::S* __restrict__ Bt,
+                                                             GemmArgs g, typename Src::Geom geo) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr int WNT = BN / 64;                       // Bt tiles of 32 rows per wave
+    constexpr int KSTEP = STEPB / sizeof(S);           // elements of K per step
+    constexpr int SLOT_A = BM * ROWB, SLOT_B = BN * ROWB;
+    constexpr int DMA_B = kDmaB<BN>;
+    // two pair slots per operand, each its own array so the compiler tells the DMA into one
+    // slot from the fragment reads of the other
+    __shared__ __align__(16) char la0[SLOT_A], la1[SLOT_A];
+    __shared__ __align__(16) char lb0[SLOT_B], lb1[SLOT_B];
+    auto slot_a = [&](auto s) -> char* {
+        if constexpr (decltype(s)::value == 0) return la0;
+        else return la1;
+    };
+    auto slot_b = [&](auto s) -> char* {
+        if constexpr (decltype(s)::value == 0) return lb0;
+        else return lb1;
+    };
+
+    uint32_t bidx, tm, tn;
+    tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, bidx, tm, tn);
+    uint64_t offA = 0, offB = 0, offC = 0;                // batch offsets
+    {
+        uint32_t rem = bidx;
+        for (int d = g.bd.n - 1; d >= 0; --d) {
+            uint32_t q = g.bd.shape[d].div(rem);
+            uint32_t idx = rem - q * g.bd.shape[d].d;
+            rem = q;
+            offA += (uint64_t)idx * g.bd.sA[d];
+            offB += (uint64_t)idx * g.bd.sB[d];
+            offC += (uint64_t)idx * g.bd.sC[d];
+        }
+    }
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const S* Abat = A + offA;
+    const S* Bblk = Bt + offB + (uint64_t)n0 * g.ldb;
+    const uint32_t rows_a = g.M - m0 < (uint32_t)BM ? g.M - m0 : (uint32_t)BM;
+    const uint32_t rows_b = g.N - n0 < (uint32_t)BN ? g.N - n0 : (uint32_t)BN;
+
+    // the wave index is wave-uniform: keeping it in a scalar register keeps every LDS slot
+    // address derived from it (the DMA destinations) scalar too
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    f16v acc[4][WNT];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    const uint32_t KT = (g.K + KSTEP - 1) / KSTEP;
+    const uint32_t KP = VEC ? g.K / (2 * KSTEP) : 0;   // whole K pairs copied by LDS DMA
+    // Fragments are double-buffered in registers: f0 holds a pair's first step, f1 its second;
+    // each step reads the next step's fragments while its own MFMAs run.
+    Frags<DT, WNT> f0, f1;
+    const auto sa = Src::template a_init<S>(g, geo, m0, rows_a, wave, lane);
+    const DmaOffsets<DMA_B> ob = dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
+    auto dma_pair = [&](auto s, uint32_t p) {
+        Src::template a_dma<S>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
+        dma_rows<S, DMA_B>(slot_b(s), Bblk, ob, p * 2 * KSTEP, wave);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    constexpr int PER_PAIR = DMA_A + DMA_B;              // DMA instructions per wave per pair
+    // Pair p lives in slot p % 2.  Its first step reads the second step's fragments (same slot,
+    // already landed) while the first step's MFMAs run; no barrier.  Its second step runs half of
+    // its MFMAs, waits for pair p + 1's DMA (the only one in flight), and meets the barrier --
+    // after which every wave has read all of pair p's fragments -- then refills slot p % 2 with
+    // pair p + 2 and reads pair p + 1's first fragments under the remaining MFMAs.  Steady pairs
+    // have no branches, so the compiler's own wait bookkeeping stays exact; sched_barrier(0)
+    // fences keep each phase's instructions inside it.
+    auto pair_steady = [&](auto s, uint32_t p) {
+        using SN = std::integral_constant<int, 1 - decltype(s)::value>;
+        constexpr int MF = kMfmaPerSlot<DT>;
+        read_frags<DT, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
+        mma_step<DT, WNT>(acc, f0);
+        interleave_even<DT, WNT>();
+        __builtin_amdgcn_sched_barrier(0);
+        mma_step<DT, WNT, 0, 2>(acc, f1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * WNT * MF, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmem<0>();
+        ring_barrier();
+        dma_pair(s, p + 2);
+        read_frags<DT, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+        mma_step<DT, WNT, 2, 4>(acc, f1);
+        interleave_odd<DT, WNT, BN>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // the last pairs: no DMA past the end, no barrier after the last
+    auto pair_drain = [&](auto s, uint32_t p) {
+        using SN = std::integral_constant<int, 1 - decltype(s)::value>;
+        if (p >= KP) return;
+        read_frags<DT, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
+        mma_step<DT, WNT>(acc, f0);
+        mma_step<DT, WNT, 0, 2>(acc, f1);
+        // (the MFMA sequence is the same on both paths: a branch around MFMAs makes the
+        // compiler shuffle the accumulators between register files)
+        if (p + 1 < KP) {
+            wait_vmem<0>();
+            ring_barrier();
+            if (p + 2 < KP) dma_pair(s, p + 2);
+            read_frags<DT, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+        }
+        mma_step<DT, WNT, 2, 4>(acc, f1);
+    };
+    if (KP > 0) {
+        dma_pair(I0{}, 0);
+        if (KP > 1) {
+            dma_pair(I1{}, 1);
+            wait_vmem<PER_PAIR>();
+        } else {
+            wait_vmem<0>();
+        }
+        ring_barrier();
+        read_frags<DT, WNT, 0>(f0, la0, lb0, wm, wn, lane);
+        uint32_t p = 0;
+        for (; p + 4 <= KP; p += 2) {                    // pairs p, p + 1 issue p + 2, p + 3
+            pair_steady(I0{}, p);
+            pair_steady(I1{}, p + 1);
+        }
+        // p is even here; at most 3 pairs remain
+        pair_drain(I0{}, p);
+        pair_drain(I1{}, p + 1);
+        pair_drain(I0{}, p + 2);
+        __syncthreads();                                  // every wave is done with the slots
+    }
+    if constexpr (Src::kStrided) {
+        // K tail (and every step of strided operands): element loads through registers into the
+        // first half of slot 0, zero past K.
+        const S* Ablk = Abat + (uint64_t)m0 * g.lda;
+        for (uint32_t kt = 2 * KP; kt < KT; kt++) {
+            uint4 ra[kTailChunks<BM>], rb[kTailChunks<BN>];
+            load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, g.K);
+            load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, g.K);
+            store_tile<BM>(la0, ra);
+            store_tile<BN>(lb0, rb);
+            __syncthreads();
+            read_frags<DT, WNT, 0>(f0, la0, lb0, wm, wn, lane);
+            mma_step<DT, WNT>(acc, f0);
+            __syncthreads();
+        }
+    }
+
+    // epilogue: acc[i][j][4 q + e] is C[row, col] with row = 32 i + lane % 32 and
+    // col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
+    S* Cbat = C + offC;
+    const int h = lane >> 5, c32 = lane & 31;
+    auto cvt = [](float v) -> S {
+        if constexpr (DT == MX_FLOAT32) return v;
+        else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
+        else return float_to_bf16(v);
+    };
+    const bool vec_store = g.cn == 1 && Src::template row_vec_ok<S>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
+    if (m0 + BM <= g.M && n0 + BN <= g.N && vec_store) {   // interior tile: 4 columns per store
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t row = m0 + wm * 128 + i * 32 + c32;
+            S* crow = Cbat + Src::row_off(g, geo, row) + n0 + wn * (WNT * 32) + 4 * h;
+#pragma unroll
+            for (int j = 0; j < WNT; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    S* p = crow + j * 32 + 8 * q;
+                    if constexpr (DT == MX_FLOAT32) {
+                        *reinterpret_cast<float4*>(p) =
+                            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                    } else {
+                        uint2 v;
+                        v.x = (uint32_t)cvt(acc[i][j][4 * q]) | ((uint32_t)cvt(acc[i][j][4 * q + 1]) << 16);
+                        v.y = (uint32_t)cvt(acc[i][j][4 * q + 2]) | ((uint32_t)cvt(acc[i][j][4 * q + 3]) << 16);
+                        *reinterpret_cast<uint2*>(p) = v;
+                    }
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t row = m0 + wm * 128 + i * 32 + c32;
+        if (row >= g.M) continue;
+        S* crow = Cbat + Src::row_off(g, geo, row);
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t col = n0 + wn * (WNT * 32) + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                if (col < g.N) crow[(uint64_t)col * g.cn] = cvt(acc[i][j][r]);
+            }
+    }
+}
+
+// A strided matrix operand (batched MatMul).
+struct MatrixSrc {
+    struct Geom {};
+    static constexpr bool kStrided = true;
+    template <typename S>
+    __device__ __forceinline__ static DmaOffsets<DMA_A> a_init(const GemmArgs& g, const Geom&, uint32_t m0,
+                                                               uint32_t rows_a, int wave, int lane) {
+        return dma_offsets<S, DMA_A>(rows_a, g.lda, wave, lane);
+    }
+    template <typename S>
+    __device__ __forceinline__ static void a_dma(char* lds, const S* Abat, const DmaOffsets<DMA_A>& o,
+                                                 const GemmArgs& g, const Geom&, uint32_t m0, uint32_t p, int wave,
+                                                 int lane) {
+        constexpr int KSTEP = STEPB / sizeof(S);
+        dma_rows<S, DMA_A>(lds, Abat + (uint64_t)m0 * g.lda, o, p * 2 * KSTEP, wave);
+    }
+    __device__ __forceinline__ static uint64_t row_off(const GemmArgs& g, const Geom&, uint32_t row) {
+        return (uint64_t)row * g.ldc;
+    }
+    template <typename S>
+    __device__ __forceinline__ static bool row_vec_ok(const GemmArgs& g, const Geom&) {
+        return ((uint64_t)g.ldc * sizeof(S)) % 16 == 0;
+    }
+};
+
+}  // namespace tile
+}  // namespace mx
