@@ -46,7 +46,7 @@ struct ConvSrc {
     static constexpr bool kStrided = false;
     // Per DMA instruction: the row's image offset (n, o * stride, and the lane's chunk folded
     // in) and its strided spatial position packed 16 bits per axis.
-    struct AState { int32_t base[tile::DMA_A]; uint32_t pos[tile::DMA_A]; };
+    template <int NA> struct AState { int32_t base[NA]; uint32_t pos[NA]; };
 
     __device__ __forceinline__ static void decompose(const Geom& geo, uint32_t m, uint32_t (&o)[NS], uint32_t& n) {
 #pragma unroll
@@ -58,14 +58,14 @@ struct ConvSrc {
         n = m;
     }
 
-    template <typename S>
-    __device__ __forceinline__ static AState a_init(const GemmArgs& g, const Geom& geo, uint32_t m0, uint32_t rows_a,
-                                                    int wave, int lane) {
+    template <typename S, int NA>
+    __device__ __forceinline__ static AState<NA> a_init(const GemmArgs& g, const Geom& geo, uint32_t m0,
+                                                        uint32_t rows_a, int wave, int lane) {
         constexpr int CE = 16 / sizeof(S);
-        AState st;
+        AState<NA> st;
 #pragma unroll
-        for (int i = 0; i < tile::DMA_A; i++) {
-            const int r = tile::dma_row(wave, i, tile::DMA_A, lane);
+        for (int i = 0; i < NA; i++) {
+            const int r = tile::dma_row(wave, i, NA, lane);
             const uint32_t m = m0 + min((uint32_t)r, rows_a - 1);
             uint32_t o[NS], n;
             decompose(geo, m, o, n);
@@ -83,8 +83,8 @@ struct ConvSrc {
         return st;
     }
 
-    template <typename S>
-    __device__ __forceinline__ static void a_dma(char* lds, const S* Abat, const AState& st, const GemmArgs& g,
+    template <typename S, int NA>
+    __device__ __forceinline__ static void a_dma(char* lds, const S* Abat, const AState<NA>& st, const GemmArgs& g,
                                                  const Geom& geo, uint32_t m0, uint32_t p, int wave, int lane) {
         constexpr int PE = tile::ROWB / sizeof(S);       // K elements per pair
         // wave-uniform: kernel position and channel block of pair p
@@ -101,7 +101,7 @@ struct ConvSrc {
             uoff += kk[d] * (int32_t)geo.xs[d];
         }
 #pragma unroll
-        for (int i = 0; i < tile::DMA_A; i++) {
+        for (int i = 0; i < NA; i++) {
             bool valid = true;
 #pragma unroll
             for (int d = 0; d < NS; d++) {
@@ -109,7 +109,7 @@ struct ConvSrc {
                 valid = valid && (uint32_t)s < geo.idim[d];
             }
             const S* src = Abat + (st.base[i] + uoff);
-            tile::dma16(valid ? (const void*)src : (const void*)g_zero_page, lds + (wave * tile::DMA_A + i) * 1024);
+            tile::dma16(valid ? (const void*)src : (const void*)g_zero_page, lds + (wave * NA + i) * 1024);
         }
     }
 
@@ -470,19 +470,8 @@ int launch_implicit_gemm(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, c
         g.bd.sB[0] = cs.Og * g.K;
         g.bd.sC[0] = (uint32_t)(cs.Og * cs.out_s[NS + 1]);
     }
-    auto go = [&](auto bn) -> int {
-        constexpr int BN = decltype(bn)::value;
-        g.tiles_m = (g.M + tile::BM - 1) / tile::BM;
-        g.tiles_n = (g.N + BN - 1) / BN;
-        const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches;
-        if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: grid too large");
-        hipLaunchKernelGGL((tile::mfma_tile_kernel<DT, BN, true, ConvSrc<NS>>), dim3((uint32_t)blocks),
-                           dim3(tile::NTHREADS), 0, st, (S*)out, (const S*)xp, (const S*)wp, g, geo);
-        MX_HIP(hipGetLastError());
-        return MX_OK;
-    };
-    if (g.N <= 128) return go(std::integral_constant<int, 128>{});
-    return go(std::integral_constant<int, 256>{});
+    return tile::launch_tile_kernel<DT, true, false, ConvSrc<NS>>(tile::choose_tile(g.M, g.N, g.batches), g, geo,
+                                                                  out, xp, wp, st, "mx_launch_conv_nd");
 }
 
 template <int DT>

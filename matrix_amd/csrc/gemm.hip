@@ -56,37 +56,87 @@ __global__ __launch_bounds__(256) void gemm_scalar_kernel(typename dt_traits<DT>
     }
 }
 
-template <int DT, int BN>
-int launch_mfma_bn(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
+// Split-K combine: C[b, m, n] = round(sum over s of P[s][b][m][n]), splits in order.
+template <int DT>
+__global__ __launch_bounds__(256) void splitk_sum_kernel(typename MmaTraits<DT>::S* __restrict__ C,
+                                                         const float* __restrict__ P, uint32_t nsplit, GemmArgs g,
+                                                         FastDiv fn, FastDiv fm) {
+    using S = typename MmaTraits<DT>::S;
+    const uint64_t per = (uint64_t)g.batches * g.M * g.N;
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= per) return;
+    float acc = P[t];
+    for (uint32_t s = 1; s < nsplit; s++) acc += P[(uint64_t)s * per + t];
+    const uint32_t tt = (uint32_t)t;                     // the launcher keeps per < 2^32
+    uint32_t q = fn.div(tt);
+    const uint32_t n = tt - q * g.N;
+    uint32_t b = fm.div(q);
+    const uint32_t m = q - b * g.M;
+    uint64_t offC = 0;
+    for (int d = g.bd.n - 1; d >= 0; --d) {
+        const uint32_t qq = g.bd.shape[d].div(b);
+        offC += (uint64_t)(b - qq * g.bd.shape[d].d) * g.bd.sC[d];
+        b = qq;
+    }
+    S v;
+    if constexpr (DT == MX_FLOAT32) v = acc;
+    else if constexpr (DT == MX_FLOAT16) v = float_to_half_bits(acc);
+    else v = float_to_bf16(acc);
+    C[offC + (uint64_t)m * g.ldc + (uint64_t)n * g.cn] = v;
+}
+
+// Split-K when the output tiles leave most of the 256 CUs idle: enough K pieces (each at least
+// four 128-byte K pairs) to give about two blocks per CU.  Returns 1 for no split.
+uint32_t choose_split(const tile::TileShape& ts, const GemmArgs& g, uint32_t pair_elems, uint32_t* ksplit) {
+    const uint64_t tiles = (uint64_t)((g.M + ts.bm - 1) / ts.bm) * ((g.N + ts.bn - 1) / ts.bn) * g.batches;
+    const uint32_t pairs = g.K / pair_elems;
+    if (tiles >= 256 || pairs < 8) return 1;
+    uint64_t want = (512 + tiles - 1) / tiles;
+    if (want > pairs / 4) want = pairs / 4;
+    if (want < 2) return 1;
+    const uint32_t pairs_per = (uint32_t)((pairs + want - 1) / want);
+    *ksplit = pairs_per * pair_elems;
+    return (g.K + *ksplit - 1) / *ksplit;
+}
+
+template <int DT>
+int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
     using S = typename MmaTraits<DT>::S;
     constexpr int CE = 16 / sizeof(S);
+    const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
+    uint32_t ksplit = 0;
+    const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
+    const uint64_t per = (uint64_t)g.batches * g.M * g.N;
     // the DMA path addresses a tile's rows with 32-bit byte offsets
     const bool vec = g.ka == 1 && g.kb == 1 && g.lda % CE == 0 && g.ldb % CE == 0 &&
-                     (uint64_t)tile::BM * g.lda * sizeof(S) < (1ull << 32) &&
-                     (uint64_t)BN * g.ldb * sizeof(S) < (1ull << 32) &&
+                     (uint64_t)ts.bm * g.lda * sizeof(S) < (1ull << 32) &&
+                     (uint64_t)ts.bn * g.ldb * sizeof(S) < (1ull << 32) &&
                      (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0 && [&] {
                          for (int d = 0; d < g.bd.n; d++)
                              if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
                          return true;
                      }();
-    g.tiles_m = (g.M + tile::BM - 1) / tile::BM;
-    g.tiles_n = (g.N + BN - 1) / BN;
-    const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches;
-    if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: grid too large");
-    tile::MatrixSrc::Geom geo{};
-    if (vec)
-        hipLaunchKernelGGL((tile::mfma_tile_kernel<DT, BN, true, tile::MatrixSrc>), dim3((uint32_t)blocks),
-                           dim3(tile::NTHREADS), 0, st, (S*)C, (const S*)A, (const S*)Bt, g, geo);
-    else
-        hipLaunchKernelGGL((tile::mfma_tile_kernel<DT, BN, false, tile::MatrixSrc>), dim3((uint32_t)blocks),
-                           dim3(tile::NTHREADS), 0, st, (S*)C, (const S*)A, (const S*)Bt, g, geo);
-    MX_HIP(hipGetLastError());
-    return MX_OK;
-}
-
-template <int DT>
-int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
-    return g.N <= 128 ? launch_mfma_bn<DT, 128>(g, C, A, Bt, st) : launch_mfma_bn<DT, 256>(g, C, A, Bt, st);
+    const tile::MatrixSrc::Geom geo{};
+    const char* who = "mx_launch_batched_matmul";
+    if (nsplit > 1 && per < 0xffffffffull) {
+        // fp32 partials [split][batch][M][N] in the stream's scratch, then an ordered sum
+        void* P = nullptr;
+        int rc = stream_scratch(st, (size_t)nsplit * per * sizeof(float), &P);
+        if (rc) return rc;
+        GemmArgs gp = g;
+        gp.ksplit = ksplit;
+        gp.ldc = g.N;
+        gp.cn = 1;
+        rc = vec ? tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit)
+                 : tile::launch_tile_kernel<DT, false, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit);
+        if (rc) return rc;
+        hipLaunchKernelGGL((splitk_sum_kernel<DT>), dim3((uint32_t)((per + 255) / 256)), dim3(256), 0, st, (S*)C,
+                           (const float*)P, nsplit, g, FastDiv(g.N), FastDiv(g.M));
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    }
+    if (vec) return tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
+    return tile::launch_tile_kernel<DT, false, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
 }
 
 template <int DT>

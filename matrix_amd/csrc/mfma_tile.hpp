@@ -6,8 +6,8 @@
 // Matrix.mm:12274-12277).  float16 / bfloat16: v_mfma_f32_32x32x16_{f16,bf16}, fp32
 // accumulation, one rounding on store.  float32: v_mfma_f32_32x32x2_f32.
 //
-// Tiling: a 256-thread block computes a 256 x BN tile of C (BN = 256 or 128) as 2 x 2 waves of
-// 128 x BN/2 (4 x BN/64 MFMA tiles of 32 x 32 per wave, fp32 accumulators in AGPRs).  A K step
+// Tiling: a 256-thread block computes a BM x BN tile of C (each 256 or 128) as 2 x 2 waves of
+// BM/2 x BN/2 (BM/64 x BN/64 MFMA tiles of 32 x 32 per wave, fp32 accumulators in AGPRs).  A K step
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
@@ -31,15 +31,13 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef __bf16 b8v __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256;
 constexpr int STEPB = 64;                 // bytes of K per row in one K step (one MFMA round)
 constexpr int ROWB = 2 * STEPB;           // bytes of one LDS row: a K pair, one 128-byte line
 constexpr int CPR = ROWB / 16;            // 16-byte chunks per LDS row
 constexpr int STEP_CHUNKS = STEPB / 16;
 constexpr int NTHREADS = 256;
 constexpr int NUM_XCD = 8;
-constexpr int DMA_A = BM * ROWB / 1024 / 4;            // 1 KB DMA instructions per wave, A slot
-template <int BN> constexpr int kDmaB = BN * ROWB / 1024 / 4;
+template <int ROWS> constexpr int kDma = ROWS * ROWB / 1024 / 4;   // 1 KB DMAs per wave per slot
 
 template <int DT> struct MmaTraits;
 template <> struct MmaTraits<MX_FLOAT16> { using S = uint16_t; };
@@ -58,6 +56,7 @@ struct GemmArgs {
     uint32_t ka, kb;              // K strides of A and Bt (1 on the DMA path)
     uint32_t ldc, cn;             // C strides: row (M) and column (N)
     uint32_t tiles_m, tiles_n, batches;
+    uint32_t ksplit;              // split-K: K elements per split (the split kernels only)
     BatchDesc bd;
 };
 
@@ -115,27 +114,30 @@ __device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[kTailChun
     }
 }
 
-// One K step's operand fragments for one wave (4 A tiles, WNT Bt tiles of 32 rows).  The step
+// One K step's operand fragments for one wave (TM A tiles, WNT Bt tiles of 32 rows).  The step
 // is half HALF of the LDS rows (logical chunks 4 HALF .. 4 HALF + 3).  16-bit types: a K block
 // is 16 elements = 2 chunks; lane half h holds chunk 2 kb + h of the step.  fp32: the step is
 // one K block of 16 elements = 4 chunks; lane half h holds chunks 2h, 2h + 1 (K offsets
 // 8h .. 8h + 7); MFMA substep s consumes element s, so the two lane halves supply k = s and
 // k = 8 + s.
-template <int DT, int WNT> struct Frags;
-template <int WNT> struct Frags<MX_FLOAT16, WNT> { static constexpr int KB = 2; h8v a[KB][4], b[KB][WNT]; };
-template <int WNT> struct Frags<MX_BFLOAT16, WNT> { static constexpr int KB = 2; b8v a[KB][4], b[KB][WNT]; };
-template <int WNT> struct Frags<MX_FLOAT32, WNT> { static constexpr int KB = 1; float4 a[KB][4][2], b[KB][WNT][2]; };
+template <int DT, int TM, int WNT> struct Frags;
+template <int TM, int WNT> struct Frags<MX_FLOAT16, TM, WNT> { static constexpr int KB = 2; h8v a[KB][TM], b[KB][WNT]; };
+template <int TM, int WNT> struct Frags<MX_BFLOAT16, TM, WNT> { static constexpr int KB = 2; b8v a[KB][TM], b[KB][WNT]; };
+template <int TM, int WNT> struct Frags<MX_FLOAT32, TM, WNT> {
+    static constexpr int KB = 1;
+    float4 a[KB][TM][2], b[KB][WNT][2];
+};
 
-template <int DT, int WNT, int HALF>
-__device__ __forceinline__ void read_frags(Frags<DT, WNT>& f, const char* la, const char* lb, int wm, int wn,
+template <int DT, int TM, int WNT, int HALF>
+__device__ __forceinline__ void read_frags(Frags<DT, TM, WNT>& f, const char* la, const char* lb, int wm, int wn,
                                            int lane) {
     const int r32 = lane & 31, h = lane >> 5;
     constexpr int C0 = HALF * STEP_CHUNKS;
 #pragma unroll
-    for (int kb = 0; kb < Frags<DT, WNT>::KB; kb++) {
+    for (int kb = 0; kb < Frags<DT, TM, WNT>::KB; kb++) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int ra = wm * 128 + t * 32 + r32;
+        for (int t = 0; t < TM; t++) {
+            const int ra = wm * (TM * 32) + t * 32 + r32;
             if constexpr (DT == MX_FLOAT32) {
 #pragma unroll
                 for (int u = 0; u < 2; u++)
@@ -165,14 +167,14 @@ __device__ __forceinline__ float f4_at(const float4 (&v)[2], int s) {
     switch (s & 3) { case 0: return q.x; case 1: return q.y; case 2: return q.z; default: return q.w; }
 }
 
-// MFMAs of the step for A tile rows I0 .. I1 - 1 of the wave's 4 x WNT grid.  The Bt fragment
+// MFMAs of the step for A tile rows I0 .. I1 - 1 of the wave's TM x WNT grid.  The Bt fragment
 // goes in the MFMA's first operand slot and the A fragment in the second, so the 32 x 32 result
 // is the C^T tile: lane l holds C row (l % 32) and, in acc[4 q .. 4 q + 3], the 4 consecutive C
 // columns 8 q + 4 (l / 32) .. + 3 -- one vector store per (q) in the epilogue.
-template <int DT, int WNT, int I0 = 0, int I1 = 4>
-__device__ __forceinline__ void mma_step(f16v (&acc)[4][WNT], const Frags<DT, WNT>& f) {
+template <int DT, int TM, int WNT, int I0, int I1>
+__device__ __forceinline__ void mma_step(f16v (&acc)[TM][WNT], const Frags<DT, TM, WNT>& f) {
 #pragma unroll
-    for (int kb = 0; kb < Frags<DT, WNT>::KB; kb++) {
+    for (int kb = 0; kb < Frags<DT, TM, WNT>::KB; kb++) {
         if constexpr (DT == MX_FLOAT32) {
 #pragma unroll
             for (int s = 0; s < 8; s++)
@@ -245,28 +247,29 @@ __device__ __forceinline__ void wait_vmem() {
 // Instruction order within a K step, so the LDS and the memory pipeline work under the matrix
 // core instead of before it (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read, 0x020
 // vector-memory read).  A slot is one MFMA for 16-bit types and four for fp32; a step has
-// 8 WNT slots, 2 (4 + WNT) fragment reads, and a pair DMA_A + kDmaB instructions per wave.
-// The fragment reads go out early in their window so that they have returned (LDS latency is
-// several MFMAs) before the next step's first MFMA needs them.
+// 2 TM WNT slots, 2 (TM + WNT) fragment reads, and a pair kDma<BM> + kDma<BN> instructions per
+// wave.  The fragment reads go out early in their window so that they have returned (LDS
+// latency is several MFMAs) before the next step's first MFMA needs them.
 template <int DT> constexpr int kMfmaPerSlot = DT == MX_FLOAT32 ? 4 : 1;
 
 // First step of a pair: the next step's fragment reads, one per leading MFMA slot.
-template <int DT, int WNT>
+template <int DT, int TM, int WNT>
 __device__ __forceinline__ void interleave_even() {
-    constexpr int MF = kMfmaPerSlot<DT>, SLOTS = 8 * WNT, NR = 2 * (4 + WNT);
+    constexpr int MF = kMfmaPerSlot<DT>, SLOTS = 2 * TM * WNT, NR = 2 * (TM + WNT);
+    static_assert(NR <= SLOTS, "interleave counts");
 #pragma unroll
     for (int i = 0; i < NR; i++) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, (SLOTS - NR) * MF, 0);
+    if constexpr (SLOTS > NR) __builtin_amdgcn_sched_group_barrier(0x008, (SLOTS - NR) * MF, 0);
 }
 
-// Second step of a pair, after its barrier (4 WNT slots left): the next step's fragment reads
+// Second step of a pair, after its barrier (TM WNT slots left): the next step's fragment reads
 // over the first half of the slots, the DMA of the pair two ahead over all of them.
-template <int DT, int WNT, int BN>
+template <int DT, int TM, int WNT, int BM, int BN>
 __device__ __forceinline__ void interleave_odd() {
-    constexpr int MF = kMfmaPerSlot<DT>, H = 4 * WNT, NR = 2 * (4 + WNT), ND = DMA_A + kDmaB<BN>;
+    constexpr int MF = kMfmaPerSlot<DT>, H = TM * WNT, NR = 2 * (TM + WNT), ND = kDma<BM> + kDma<BN>;
     constexpr int RPS = NR / (H / 2);                          // reads per slot, first half
     constexpr int D1 = (ND + H - 1) / H;                       // DMAs per slot, first half
     constexpr int D2 = (ND - D1 * (H / 2)) / (H / 2);          // DMAs per slot, second half
@@ -303,20 +306,28 @@ __device__ __forceinline__ void ring_barrier() {
 // Src provides:
 //   Geom                                  extra kernel argument (empty for GEMM)
 //   static constexpr bool kStrided        A may take the guarded K-tail path
-//   AState a_init<S>(g, geo, m0, wave, lane)          per-lane A addressing state
-//   void a_dma<S>(lds, A, st, g, geo, m0, pair, wave, lane)   one pair of the A slot
+//   AState a_init<S, NA>(g, geo, m0, rows_a, wave, lane)    per-lane A addressing state
+//   void a_dma<S, NA>(lds, A, st, g, geo, m0, pair, wave, lane)   one pair of the A slot
 //   uint64_t row_off(g, geo, row)         element offset of C row `row` (batch offset apart)
 //   bool row_vec_ok<S>(g, geo)            every row offset is a multiple of 16 bytes
-template <int DT, int BN, bool VEC, class Src>
-__global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<DT>::S* __restrict__ C,
+// (NA = DMA instructions per wave for the A slot.)  Tiles are BM x BN with BM, BN in {128, 256}:
+// 2 x 2 waves of (BM / 2) x (BN / 2).  A 128 x 128 tile needs 64 KB of LDS, so two blocks share
+// a CU.
+// SPLIT: the K range is cut into g.ksplit-element pieces, one per block along the outermost
+// block-batch index; the block writes its fp32 partial tile to Cv as [split][batch][M][N]
+// (g.ldc = N, g.cn = 1), and a second kernel sums the splits in order.
+template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src>
+__global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ Cv,
                                                              const typename MmaTraits<DT>::S* __restrict__ A,
                                                              const typename MmaTraits<DT>::S* __restrict__ Bt,
                                                              GemmArgs g, typename Src::Geom geo) {
     using S = typename MmaTraits<DT>::S;
+    using CT = std::conditional_t<SPLIT, float, S>;    // element type written to Cv
+    constexpr int TM = BM / 64;                        // A tiles of 32 rows per wave
     constexpr int WNT = BN / 64;                       // Bt tiles of 32 rows per wave
     constexpr int KSTEP = STEPB / sizeof(S);           // elements of K per step
     constexpr int SLOT_A = BM * ROWB, SLOT_B = BN * ROWB;
-    constexpr int DMA_B = kDmaB<BN>;
+    constexpr int DMA_A = kDma<BM>, DMA_B = kDma<BN>;
     // two pair slots per operand, each its own array so the compiler tells the DMA into one
     // slot from the fragment reads of the other
     __shared__ __align__(16) char la0[SLOT_A], la1[SLOT_A];
@@ -333,6 +344,16 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
     uint32_t bidx, tm, tn;
     tile_of(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, bidx, tm, tn);
     uint64_t offA = 0, offB = 0, offC = 0;                // batch offsets
+    uint32_t Klen = g.K;                                  // this block's K range: kbeg .. + Klen
+    if constexpr (SPLIT) {
+        const uint32_t split = bidx / g.batches;
+        bidx -= split * g.batches;
+        const uint32_t kbeg = split * g.ksplit;
+        Klen = g.K - kbeg < g.ksplit ? g.K - kbeg : g.ksplit;
+        offA = (uint64_t)kbeg * g.ka;
+        offB = (uint64_t)kbeg * g.kb;
+        offC = ((uint64_t)split * g.batches + bidx) * g.M * g.N;
+    }
     {
         uint32_t rem = bidx;
         for (int d = g.bd.n - 1; d >= 0; --d) {
@@ -341,7 +362,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
             rem = q;
             offA += (uint64_t)idx * g.bd.sA[d];
             offB += (uint64_t)idx * g.bd.sB[d];
-            offC += (uint64_t)idx * g.bd.sC[d];
+            if constexpr (!SPLIT) offC += (uint64_t)idx * g.bd.sC[d];
         }
     }
     const uint32_t m0 = tm * BM, n0 = tn * BN;
@@ -355,25 +376,26 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
 
-    f16v acc[4][WNT];
+    f16v acc[TM][WNT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < WNT; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    const uint32_t KT = (g.K + KSTEP - 1) / KSTEP;
-    const uint32_t KP = VEC ? g.K / (2 * KSTEP) : 0;   // whole K pairs copied by LDS DMA
+    const uint32_t KT = (Klen + KSTEP - 1) / KSTEP;
+    const uint32_t KP = VEC ? Klen / (2 * KSTEP) : 0;  // whole K pairs copied by LDS DMA
     // Fragments are double-buffered in registers: f0 holds a pair's first step, f1 its second;
     // each step reads the next step's fragments while its own MFMAs run.
-    Frags<DT, WNT> f0, f1;
-    const auto sa = Src::template a_init<S>(g, geo, m0, rows_a, wave, lane);
+    Frags<DT, TM, WNT> f0, f1;
+    const auto sa = Src::template a_init<S, DMA_A>(g, geo, m0, rows_a, wave, lane);
     const DmaOffsets<DMA_B> ob = dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
     auto dma_pair = [&](auto s, uint32_t p) {
-        Src::template a_dma<S>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
+        Src::template a_dma<S, DMA_A>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
         dma_rows<S, DMA_B>(slot_b(s), Bblk, ob, p * 2 * KSTEP, wave);
     };
+    constexpr int H0 = TM / 2;                           // A tile rows of a step's first half
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     constexpr int PER_PAIR = DMA_A + DMA_B;              // DMA instructions per wave per pair
@@ -387,37 +409,37 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
     auto pair_steady = [&](auto s, uint32_t p) {
         using SN = std::integral_constant<int, 1 - decltype(s)::value>;
         constexpr int MF = kMfmaPerSlot<DT>;
-        read_frags<DT, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
-        mma_step<DT, WNT>(acc, f0);
-        interleave_even<DT, WNT>();
+        read_frags<DT, TM, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
+        mma_step<DT, TM, WNT, 0, TM>(acc, f0);
+        interleave_even<DT, TM, WNT>();
         __builtin_amdgcn_sched_barrier(0);
-        mma_step<DT, WNT, 0, 2>(acc, f1);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4 * WNT * MF, 0);
+        mma_step<DT, TM, WNT, 0, H0>(acc, f1);
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * WNT * MF, 0);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmem<0>();
         ring_barrier();
         dma_pair(s, p + 2);
-        read_frags<DT, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
-        mma_step<DT, WNT, 2, 4>(acc, f1);
-        interleave_odd<DT, WNT, BN>();
+        read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+        mma_step<DT, TM, WNT, H0, TM>(acc, f1);
+        interleave_odd<DT, TM, WNT, BM, BN>();
         __builtin_amdgcn_sched_barrier(0);
     };
     // the last pairs: no DMA past the end, no barrier after the last
     auto pair_drain = [&](auto s, uint32_t p) {
         using SN = std::integral_constant<int, 1 - decltype(s)::value>;
         if (p >= KP) return;
-        read_frags<DT, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
-        mma_step<DT, WNT>(acc, f0);
-        mma_step<DT, WNT, 0, 2>(acc, f1);
+        read_frags<DT, TM, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
+        mma_step<DT, TM, WNT, 0, TM>(acc, f0);
+        mma_step<DT, TM, WNT, 0, H0>(acc, f1);
         // (the MFMA sequence is the same on both paths: a branch around MFMAs makes the
         // compiler shuffle the accumulators between register files)
         if (p + 1 < KP) {
             wait_vmem<0>();
             ring_barrier();
             if (p + 2 < KP) dma_pair(s, p + 2);
-            read_frags<DT, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+            read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
         }
-        mma_step<DT, WNT, 2, 4>(acc, f1);
+        mma_step<DT, TM, WNT, H0, TM>(acc, f1);
     };
     if (KP > 0) {
         dma_pair(I0{}, 0);
@@ -428,7 +450,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
             wait_vmem<0>();
         }
         ring_barrier();
-        read_frags<DT, WNT, 0>(f0, la0, lb0, wm, wn, lane);
+        read_frags<DT, TM, WNT, 0>(f0, la0, lb0, wm, wn, lane);
         uint32_t p = 0;
         for (; p + 4 <= KP; p += 2) {                    // pairs p, p + 1 issue p + 2, p + 3
             pair_steady(I0{}, p);
@@ -446,38 +468,38 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
         const S* Ablk = Abat + (uint64_t)m0 * g.lda;
         for (uint32_t kt = 2 * KP; kt < KT; kt++) {
             uint4 ra[kTailChunks<BM>], rb[kTailChunks<BN>];
-            load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, g.K);
-            load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, g.K);
+            load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
+            load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
             store_tile<BM>(la0, ra);
             store_tile<BN>(lb0, rb);
             __syncthreads();
-            read_frags<DT, WNT, 0>(f0, la0, lb0, wm, wn, lane);
-            mma_step<DT, WNT>(acc, f0);
+            read_frags<DT, TM, WNT, 0>(f0, la0, lb0, wm, wn, lane);
+            mma_step<DT, TM, WNT, 0, TM>(acc, f0);
             __syncthreads();
         }
     }
 
     // epilogue: acc[i][j][4 q + e] is C[row, col] with row = 32 i + lane % 32 and
     // col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
-    S* Cbat = C + offC;
+    CT* Cbat = static_cast<CT*>(Cv) + offC;
     const int h = lane >> 5, c32 = lane & 31;
-    auto cvt = [](float v) -> S {
-        if constexpr (DT == MX_FLOAT32) return v;
+    auto cvt = [](float v) -> CT {
+        if constexpr (SPLIT || DT == MX_FLOAT32) return v;
         else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
         else return float_to_bf16(v);
     };
-    const bool vec_store = g.cn == 1 && Src::template row_vec_ok<S>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
+    const bool vec_store = g.cn == 1 && Src::template row_vec_ok<CT>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
     if (m0 + BM <= g.M && n0 + BN <= g.N && vec_store) {   // interior tile: 4 columns per store
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t row = m0 + wm * 128 + i * 32 + c32;
-            S* crow = Cbat + Src::row_off(g, geo, row) + n0 + wn * (WNT * 32) + 4 * h;
+        for (int i = 0; i < TM; i++) {
+            const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+            CT* crow = Cbat + Src::row_off(g, geo, row) + n0 + wn * (WNT * 32) + 4 * h;
 #pragma unroll
             for (int j = 0; j < WNT; j++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    S* p = crow + j * 32 + 8 * q;
-                    if constexpr (DT == MX_FLOAT32) {
+                    CT* p = crow + j * 32 + 8 * q;
+                    if constexpr (sizeof(CT) == 4) {
                         *reinterpret_cast<float4*>(p) =
                             make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
                     } else {
@@ -491,10 +513,10 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
         return;
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t row = m0 + wm * 128 + i * 32 + c32;
+    for (int i = 0; i < TM; i++) {
+        const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
         if (row >= g.M) continue;
-        S* crow = Cbat + Src::row_off(g, geo, row);
+        CT* crow = Cbat + Src::row_off(g, geo, row);
 #pragma unroll
         for (int j = 0; j < WNT; j++)
 #pragma unroll
@@ -505,21 +527,55 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(typename MmaTraits<
     }
 }
 
+// Tile shape for a problem: 256-row tiles (256 x 256, or 256 x 128 when N <= 128) while they give
+// at least two waves of blocks over the 256 CUs; otherwise 128 x 128 tiles, two blocks per CU.
+struct TileShape { int bm, bn; };
+inline TileShape choose_tile(uint64_t M, uint64_t N, uint64_t batches) {
+    const int bn = N <= 128 ? 128 : 256;
+    const uint64_t big = (M + 255) / 256 * ((N + bn - 1) / bn) * batches;
+    if (big >= 512) return {256, bn};
+    return {128, 128};
+}
+
+// Launches mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src> for the chosen shape; with SPLIT,
+// nsplit K pieces of g.ksplit elements each.
+template <int DT, bool VEC, bool SPLIT, class Src>
+int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C, const void* A, const void* Bt,
+                       hipStream_t st, const char* who, uint32_t nsplit = 1) {
+    using S = typename MmaTraits<DT>::S;
+    auto go = [&](auto bm, auto bn) -> int {
+        constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
+        g.tiles_m = (g.M + BM - 1) / BM;
+        g.tiles_n = (g.N + BN - 1) / BN;
+        const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches * nsplit;
+        if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": grid too large");
+        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src>), dim3((uint32_t)blocks), dim3(NTHREADS),
+                           0, st, C, (const S*)A, (const S*)Bt, g, geo);
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    };
+    using I128 = std::integral_constant<int, 128>;
+    using I256 = std::integral_constant<int, 256>;
+    if (ts.bm == 256 && ts.bn == 256) return go(I256{}, I256{});
+    if (ts.bm == 256) return go(I256{}, I128{});
+    return go(I128{}, I128{});
+}
+
 // A strided matrix operand (batched MatMul).
 struct MatrixSrc {
     struct Geom {};
     static constexpr bool kStrided = true;
-    template <typename S>
-    __device__ __forceinline__ static DmaOffsets<DMA_A> a_init(const GemmArgs& g, const Geom&, uint32_t m0,
-                                                               uint32_t rows_a, int wave, int lane) {
-        return dma_offsets<S, DMA_A>(rows_a, g.lda, wave, lane);
+    template <typename S, int NA>
+    __device__ __forceinline__ static DmaOffsets<NA> a_init(const GemmArgs& g, const Geom&, uint32_t m0,
+                                                            uint32_t rows_a, int wave, int lane) {
+        return dma_offsets<S, NA>(rows_a, g.lda, wave, lane);
     }
-    template <typename S>
-    __device__ __forceinline__ static void a_dma(char* lds, const S* Abat, const DmaOffsets<DMA_A>& o,
+    template <typename S, int NA>
+    __device__ __forceinline__ static void a_dma(char* lds, const S* Abat, const DmaOffsets<NA>& o,
                                                  const GemmArgs& g, const Geom&, uint32_t m0, uint32_t p, int wave,
                                                  int lane) {
         constexpr int KSTEP = STEPB / sizeof(S);
-        dma_rows<S, DMA_A>(lds, Abat + (uint64_t)m0 * g.lda, o, p * 2 * KSTEP, wave);
+        dma_rows<S, NA>(lds, Abat + (uint64_t)m0 * g.lda, o, p * 2 * KSTEP, wave);
     }
     __device__ __forceinline__ static uint64_t row_off(const GemmArgs& g, const Geom&, uint32_t row) {
         return (uint64_t)row * g.ldc;

@@ -53,6 +53,40 @@ bool resolve_stream(void* in, hipStream_t* out) {
     return thread_stream(out) == MX_OK;
 }
 
+// Library-owned scratch, one buffer per stream: work queued on one stream runs in order, so
+// every launch on that stream may reuse the buffer.  Growing it waits for the stream (the old
+// buffer may still be in use by queued work) and then reallocates.
+namespace {
+struct Scratch { void* ptr = nullptr; size_t bytes = 0; };
+std::mutex g_scratch_mu;
+std::unordered_map<hipStream_t, Scratch> g_scratch;
+}  // namespace
+
+int stream_scratch(hipStream_t st, size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    Scratch& s = g_scratch[st];
+    if (s.bytes < bytes) {
+        const size_t want = bytes < (size_t)1 << 20 ? (size_t)1 << 20 : bytes + bytes / 4;
+        if (s.ptr) {
+            MX_HIP(hipStreamSynchronize(st));
+            MX_HIP(hipFree(s.ptr));
+            s.ptr = nullptr;
+            s.bytes = 0;
+        }
+        MX_HIP(hipMalloc(&s.ptr, want));
+        s.bytes = want;
+    }
+    *out = s.ptr;
+    return MX_OK;
+}
+
+static void release_scratch() {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    for (auto& kv : g_scratch)
+        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+    g_scratch.clear();
+}
+
 }  // namespace mx
 
 using namespace mx;
@@ -94,6 +128,7 @@ int mx_hip_shutdown(void) {
         (void)hipStreamDestroy(kv.second);
     }
     g_streams.clear();
+    release_scratch();
     g_device.store(-1);
     return rc;
 }

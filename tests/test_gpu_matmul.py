@@ -107,6 +107,37 @@ def test_skinny_matmul(mx, orc):
         assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= tol
 
 
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
+    ([100, 3000], [70, 3000]),           # one tile, long ragged K: many K splits, short last split
+    ([512, 4096], [10, 4096]),           # the MLP's 10-wide output layer
+    ([4, 3, 2000], [2000, 2000]),        # batch folded into M, split K
+    ([2, 64, 1000], [2, 96, 1000]),      # per-batch Bt, split K with two batches
+])
+def test_split_k(mx, orc, dt, case):
+    """Few output tiles and a long K: the K range is split over blocks and summed in order."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(12)
+    a_shape, bt_shape = case
+    K = a_shape[-1]
+    a = gen(rng, code, a_shape, 1.0 / math.sqrt(K), mx)
+    bt = gen(rng, code, bt_shape, 1.0, mx)
+    got, ref, _ = run_mm(mx, orc, code, a, bt)
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
+    got2, _, _ = run_mm(mx, orc, code, a, bt)          # deterministic: the same bits again
+    assert np.array_equal(got, got2)
+
+
+def test_split_k_strided(mx, orc):
+    """A transposed A (scalar-load path) with a split K range."""
+    rng = np.random.default_rng(13)
+    base = rng.standard_normal([2500, 40]).astype(np.float32)   # A = base.T : [40, 2500], strides [1, 40]
+    bt = rng.standard_normal([24, 2500]).astype(np.float32)
+    got, _, _ = run_mm(mx, orc, mx.FLOAT32, base, bt, a_shape=[40, 2500], a_strides=[1, 40])
+    ref64 = base.T.astype(np.float64) @ bt.T.astype(np.float64)
+    assert normwise_rel(got, ref64) <= 1e-5
+
+
 def test_identity_and_one_hot_exact(mx, orc):
     rng = np.random.default_rng(2)
     a = rng.standard_normal([3, 96, 80]).astype(np.float32)
