@@ -88,14 +88,49 @@ def build_oracle() -> Path:
     return ROOT / "oracle" / "_build" / "liboracle.so"
 
 
+PROGRAMS = PKG / "programs"
+BINDIR = PKG / "_bin"
+TESTS_CPP = ROOT / "tests" / "cpp"
+
+
+def _link_program(src: Path, out: Path, rpath: str) -> None:
+    out.parent.mkdir(exist_ok=True)
+    _run([CXX, *CXX_FLAGS, str(src), "-o", str(out), f"-L{LIBDIR}", "-lmatrix_amd", f"-Wl,-rpath,{rpath}",
+          "-Wl,-rpath,/opt/rocm/lib"])
+
+
+def build_programs() -> list[Path]:
+    """Workload drivers over the C++ graph API (matrix_amd/programs/*.cpp -> matrix_amd/_bin/)."""
+    outs = []
+    for src in sorted(PROGRAMS.glob("*.cpp")):
+        out = BINDIR / src.stem
+        _link_program(src, out, "$ORIGIN/../_lib")
+        outs.append(out)
+    return outs
+
+
+def build_test_programs() -> list[Path]:
+    """C++ test drivers (tests/cpp/*.cpp -> tests/cpp/_build/)."""
+    outs = []
+    for src in sorted(TESTS_CPP.glob("*.cpp")):
+        out = TESTS_CPP / "_build" / src.stem
+        _link_program(src, out, "$ORIGIN/../../../matrix_amd/_lib")
+        outs.append(out)
+    return outs
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--oracle", action="store_true", help="also build the CPU oracle")
+    ap.add_argument("--programs", action="store_true", help="also build the workload and C++ test drivers")
     ap.add_argument("-j", type=int, default=None)
     a = ap.parse_args(argv)
     print(build_kernels(a.j))
     if a.oracle:
         print(build_oracle())
+    if a.programs:
+        for p in build_programs() + build_test_programs():
+            print(p)
     return 0
 
 

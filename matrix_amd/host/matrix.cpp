@@ -1,0 +1,813 @@
+// matrix.cpp -- graph building, compile / execute, and reverse-mode autodiff for matrix.hpp.
+//
+// Node semantics follow the reference's Primitives (primitives.cpp): broadcast binary ops
+// (Addition/Subtraction/Multiplication/DivisionPrimitive 397-1046, Max/MinPrimitive
+// 2515-2824, equal Matrix.mm:14451-14540), one-axis reductions (Sum/Max/Min/ArgMax/ArgMin,
+// primitives.cpp:1967-2972, 7584-7799), DotPrimitive (5464-5626), ConvolvePrimitive (192-396),
+// AsType copies (Matrix.mm:8384-8413) and views.  Each node's compile() derives the collapsed
+// descriptors its kernel consumes (collapse_dims*, Mods/Utils.mm:114-435) and allocates its
+// output and workspace; execute() only launches.
+#include "matrix.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <mutex>
+#include <numeric>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "../../include/matrix_amd.h"
+#include "../../include/matrix_amd_shape.h"
+
+using matrix_amd::Storage;
+
+namespace {
+
+constexpr uint64_t kCap = (1ull << 31) - 1;    // collapse size cap (size_m indexing)
+
+[[noreturn]] void fail_status(int st, const std::string& what) {
+    throw std::runtime_error("matrix_amd: " + what + " failed (status " + std::to_string(st) + "): " + mx_last_error());
+}
+void check(int st, const std::string& what) {
+    if (st != MX_OK) fail_status(st, what);
+}
+
+std::vector<size_m> contiguous_strides(const std::vector<size_m>& shape) {
+    std::vector<size_m> st(shape.size());
+    uint64_t acc = 1;
+    for (int i = (int)shape.size() - 1; i >= 0; --i) {
+        st[i] = (size_m)acc;
+        acc *= shape[i];
+    }
+    return st;
+}
+
+uint64_t prod(const std::vector<size_m>& v) {
+    uint64_t p = 1;
+    for (auto x : v) p *= x;
+    return p;
+}
+
+uint16_t host_f32_to_f16(float f) {
+    _Float16 h = (_Float16)f;
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+uint16_t host_f32_to_bf16(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// One element of `type` holding `v` (static_cast semantics for the integer types).
+void store_value(dtype type, double v, uint8_t* dst) {
+    switch (type) {
+    case dtype::Float: { float f = (float)v; std::memcpy(dst, &f, 4); break; }
+    case dtype::Float16: { uint16_t h = host_f32_to_f16((float)v); std::memcpy(dst, &h, 2); break; }
+    case dtype::BFloat16: { uint16_t h = host_f32_to_bf16((float)v); std::memcpy(dst, &h, 2); break; }
+    case dtype::Int8: { int8_t x = (int8_t)(int64_t)v; std::memcpy(dst, &x, 1); break; }
+    case dtype::UInt8: { uint8_t x = (uint8_t)(int64_t)v; std::memcpy(dst, &x, 1); break; }
+    case dtype::Bool: { uint8_t x = v != 0.0; std::memcpy(dst, &x, 1); break; }
+    case dtype::Int16: { int16_t x = (int16_t)(int64_t)v; std::memcpy(dst, &x, 2); break; }
+    case dtype::UInt16: { uint16_t x = (uint16_t)(int64_t)v; std::memcpy(dst, &x, 2); break; }
+    case dtype::Int32: { int32_t x = (int32_t)(int64_t)v; std::memcpy(dst, &x, 4); break; }
+    case dtype::UInt32: { uint32_t x = (uint32_t)(int64_t)v; std::memcpy(dst, &x, 4); break; }
+    case dtype::Int64: { int64_t x = (int64_t)v; std::memcpy(dst, &x, 8); break; }
+    case dtype::UInt64: { uint64_t x = (uint64_t)v; std::memcpy(dst, &x, 8); break; }
+    default: throw std::invalid_argument("matrix: unsupported dtype");
+    }
+}
+
+int norm_axis(int axis, uint32_t dims, const char* who) {
+    if (axis < 0) axis += (int)dims;
+    if (axis < 0 || axis >= (int)dims)
+        throw std::invalid_argument(std::string("matrix::") + who + ": axis out of range for rank " + std::to_string(dims));
+    return axis;
+}
+
+// A device buffer owned by a node (workspace).
+struct DevBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    ~DevBuf() { if (p) mx_hip_free(p); }
+    void reserve(size_t b) {
+        if (b <= bytes) return;
+        if (p) { mx_hip_free(p); p = nullptr; }
+        check(mx_hip_alloc(b, &p), "workspace allocation");
+        bytes = b;
+    }
+};
+
+char* dptr(const matrix& m) {
+    if (!m.storage || !m.storage->dev) throw std::logic_error("matrix: operand has no device buffer (not compiled)");
+    return static_cast<char*>(m.storage->dev) + m.offset * dtype_size(m.type);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ dtypes, storage, device
+size_t dtype_size(dtype t) {
+    switch (t) {
+    case dtype::Float: case dtype::Int32: case dtype::UInt32: return 4;
+    case dtype::Float16: case dtype::BFloat16: case dtype::Int16: case dtype::UInt16: return 2;
+    case dtype::UInt8: case dtype::Int8: case dtype::Bool: return 1;
+    case dtype::Int64: case dtype::UInt64: case dtype::Complex64: return 8;
+    }
+    return 0;
+}
+
+const char* dtype_name(dtype t) {
+    static const char* names[] = {"Float", "Float16", "UInt8", "Int32", "Int16", "UInt32", "UInt16",
+                                  "Bool", "Int8", "Complex64", "BFloat16", "Int64", "UInt64"};
+    const unsigned i = (unsigned)t;
+    return i < 13 ? names[i] : "?";
+}
+
+namespace matrix_amd {
+namespace {
+std::once_flag g_init_once;
+int g_device = 0;
+}  // namespace
+
+void init(int device) {
+    g_device = device;
+    std::call_once(g_init_once, [] { check(mx_hip_init(g_device), "mx_hip_init"); });
+}
+
+Storage::~Storage() {
+    if (dev) mx_hip_free(dev);
+}
+
+void Storage::allocate() {
+    if (dev || bytes == 0) return;
+    init(g_device);
+    check(mx_hip_alloc(bytes, &dev), "device allocation");
+}
+
+void Storage::upload() {
+    allocate();
+    if (bytes) check(mx_hip_h2d(dev, host.data(), bytes, nullptr), "host-to-device copy");
+    dev_stale = false;
+}
+}  // namespace matrix_amd
+
+// ------------------------------------------------------------------ matrix basics
+size_t matrix::total_size() const { return (size_t)prod(shp_); }
+
+bool matrix::is_contiguous() const {
+    uint64_t want = 1;
+    for (int i = (int)dims - 1; i >= 0; --i) {
+        if (shp_[i] != 1 && str_[i] != want) return false;
+        want *= shp_[i];
+    }
+    return true;
+}
+
+matrix matrix::from_bytes(const std::vector<size_m>& shape, dtype type, const void* data) {
+    matrix m;
+    m.dims = (uint32_t)shape.size();
+    m.type = type;
+    m.shp_ = shape;
+    m.str_ = contiguous_strides(shape);
+    m.storage = std::make_shared<Storage>();
+    m.storage->bytes = (size_t)prod(shape) * dtype_size(type);
+    m.storage->host.assign(m.storage->bytes, 0);
+    if (data && m.storage->bytes) std::memcpy(m.storage->host.data(), data, m.storage->bytes);
+    m.storage->host_is_source = true;
+    return m;
+}
+
+matrix matrix::leaf(const std::vector<size_m>& shape, dtype type) { return from_bytes(shape, type, nullptr); }
+
+matrix matrix::full(const std::vector<size_m>& shape, double value, dtype type) {
+    matrix m = from_bytes(shape, type, nullptr);
+    const size_t es = dtype_size(type);
+    uint8_t one[8];
+    store_value(type, value, one);
+    for (size_t i = 0; i < m.storage->bytes; i += es) std::memcpy(m.storage->host.data() + i, one, es);
+    return m;
+}
+
+matrix matrix::scalar(double value, dtype type) { return full({}, value, type); }
+
+void* matrix::host_data() {
+    if (tape || !storage || !storage->host_is_source) throw std::logic_error("matrix::host_data: not a leaf");
+    return storage->host.data();
+}
+
+void matrix::mark_changed() {
+    if (tape || !storage) throw std::logic_error("matrix::mark_changed: not a leaf");
+    storage->dev_stale = true;
+}
+
+void* matrix::device_ptr() const { return dptr(*this); }
+
+matrix matrix::make_node(std::vector<size_m> shape, dtype type, std::shared_ptr<Primitive> prim) {
+    matrix m;
+    m.dims = (uint32_t)shape.size();
+    m.type = type;
+    m.str_ = contiguous_strides(shape);
+    m.shp_ = std::move(shape);
+    m.storage = std::make_shared<Storage>();
+    m.storage->bytes = (size_t)prod(m.shp_) * dtype_size(type);
+    m.tape = std::move(prim);
+    return m;
+}
+
+matrix matrix::make_view(const matrix& base, std::vector<size_m> shape, std::vector<size_m> strides, size_t offset,
+                         std::shared_ptr<Primitive> prim) {
+    matrix m;
+    m.dims = (uint32_t)shape.size();
+    m.type = base.type;
+    m.shp_ = std::move(shape);
+    m.str_ = std::move(strides);
+    m.offset = offset;
+    m.storage = base.storage;
+    m.tape = std::move(prim);
+    return m;
+}
+
+// ------------------------------------------------------------------ primitives
+namespace {
+
+// A view: shares its input's storage, no kernel.  vjp maps the gradient back to the input.
+struct ViewPrim : Primitive {
+    enum Kind { Transpose, Reshape, Broadcast } kind;
+    matrix in;
+    std::vector<size_m> perm;
+    ViewPrim(Kind k, matrix x, std::vector<size_m> p = {}) : kind(k), in(std::move(x)), perm(std::move(p)) {}
+    const char* name() const override { return kind == Transpose ? "Transpose" : kind == Reshape ? "Reshape" : "Broadcast"; }
+    uint32_t num_inputs() const override { return 1; }
+    matrix& input_at(uint32_t) override { return in; }
+    bool is_view() const override { return true; }
+    void compile(const matrix&) override {}
+    void execute(const matrix&) override {}
+    std::vector<matrix> vjp(matrix& g) override {
+        if (kind == Transpose) {
+            std::vector<size_m> inv(perm.size());
+            for (size_t i = 0; i < perm.size(); i++) inv[perm[i]] = (size_m)i;
+            return {g.transpose(inv)};
+        }
+        if (kind == Reshape) return {g.reshape(in.shape_vec())};
+        return {g.unbroadcast_shape(in.shape(), (int)in.dims)};
+    }
+};
+
+// Broadcast binary op (and Equal): out = a op b with NumPy broadcasting.
+struct BinaryPrim : Primitive {
+    int op;
+    matrix a, b;
+    uint32_t cd = 0;
+    uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sR[MX_MAX_DIMS];
+    BinaryPrim(int o, matrix x, matrix y) : op(o), a(std::move(x)), b(std::move(y)) {}
+    const char* name() const override {
+        static const char* n[] = {"Add", "Sub", "Mul", "Divide", "Max", "Min", "Equal"};
+        return n[op];
+    }
+    uint32_t num_inputs() const override { return 2; }
+    matrix& input_at(uint32_t i) override { return i ? b : a; }
+    void compile(const matrix& out) override {
+        uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+        check(mx_broadcast_shapes(a.shape(), a.strides(), a.dims, b.shape(), b.strides(), b.dims, os, ost, b1s, b1t, b2s,
+                                  b2t), "broadcast");
+        if (out.dims == 0) { cd = 0; return; }
+        check(mx_collapse_dims3(os, b1t, b2t, ost, out.dims, kCap, cs, sA, sB, sR, &cd), "collapse_dims");
+    }
+    void execute(const matrix& out) override {
+        check(mx_launch_bcast_binary(op, (int)a.type, (int)cd, cs, sR, sA, sB, dptr(out), dptr(a), dptr(b), nullptr),
+              std::string("launch ") + name());
+    }
+    std::vector<matrix> vjp(matrix& g) override {
+        const size_m* as = a.shape();
+        const size_m* bs = b.shape();
+        switch (op) {
+        case MX_OP_ADD: return {g.unbroadcast_shape(as, a.dims), g.unbroadcast_shape(bs, b.dims)};
+        case MX_OP_SUB: return {g.unbroadcast_shape(as, a.dims), g.unbroadcast_shape(bs, b.dims) * -1.0f};
+        case MX_OP_MUL: return {(g * b).unbroadcast_shape(as, a.dims), (g * a).unbroadcast_shape(bs, b.dims)};
+        case MX_OP_DIV: {
+            matrix ga = g / b;
+            matrix gb = (g * a) / (b * b) * -1.0f;
+            return {ga.unbroadcast_shape(as, a.dims), gb.unbroadcast_shape(bs, b.dims)};
+        }
+        case MX_OP_MAX:
+        case MX_OP_MIN: {
+            // ties send the gradient to b (primitives.cpp:2604-2608)
+            matrix mask_b = matrix::equal(b, op == MX_OP_MAX ? matrix::max(a, b) : matrix::min(a, b));
+            matrix mask_a = 1.0f - mask_b;
+            return {(g * mask_a).unbroadcast_shape(as, a.dims), (g * mask_b).unbroadcast_shape(bs, b.dims)};
+        }
+        default: return {a.zeros(), b.zeros()};
+        }
+    }
+};
+
+// One-axis reduction.
+struct ReducePrim : Primitive {
+    int op;
+    matrix in;
+    int axis;
+    bool keepdims;
+    uint32_t cd = 0, rstride = 0, n = 0;
+    uint32_t cs[MX_MAX_DIMS], sOut[MX_MAX_DIMS], sIn[MX_MAX_DIMS];
+    DevBuf ws;
+    ReducePrim(int o, matrix x, int ax, bool kd) : op(o), in(std::move(x)), axis(ax), keepdims(kd) {}
+    const char* name() const override {
+        static const char* nm[] = {"Sum", "Max", "Min", "ArgMax", "ArgMin"};
+        return nm[op];
+    }
+    uint32_t num_inputs() const override { return 1; }
+    matrix& input_at(uint32_t) override { return in; }
+    void compile(const matrix&) override {
+        // the output is contiguous; keepdims does not change its layout
+        std::vector<size_m> oshape;
+        for (uint32_t i = 0; i < in.dims; i++)
+            if ((int)i != axis) oshape.push_back(in.shape()[i]);
+        const std::vector<size_m> ost = contiguous_strides(oshape);
+        check(mx_collapse_dims_reduce2(in.shape(), ost.data(), in.strides(), in.dims, axis, 0, 1, kCap, cs, sOut, sIn,
+                                       &cd), "collapse_dims_reduce");
+        if (cd == 0) { cd = 1; cs[0] = 1; sOut[0] = 1; sIn[0] = 1; }
+        rstride = in.strides()[axis];
+        n = in.shape()[axis];
+        size_t bytes = 0;
+        check(mx_reduce_workspace_bytes(op, (int)in.type, rstride, n, (int)cd, cs, sOut, sIn, &bytes), "reduce workspace");
+        if (bytes) ws.reserve(bytes);
+    }
+    void execute(const matrix& out) override {
+        check(mx_launch_reduce(op, (int)in.type, rstride, n, (int)cd, cs, sOut, sIn, dptr(out), dptr(in), ws.p, ws.bytes,
+                               nullptr), std::string("launch ") + name());
+    }
+    std::vector<matrix> vjp(matrix& g) override {
+        if (op != MX_RED_SUM) throw std::logic_error(std::string("matrix: no vjp for ") + name());
+        matrix gg = keepdims ? g : g.unsqueeze(axis);
+        return {gg.broadcast_to(in.shape_vec())};
+    }
+};
+
+// C = A . Bt^T over the batch axes (a [..., M, K], bt [..., N, K]).
+struct DotPrim : Primitive {
+    matrix a, bt;
+    uint32_t cd = 0, K = 0;
+    uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sC[MX_MAX_DIMS];
+    DotPrim(matrix x, matrix y) : a(std::move(x)), bt(std::move(y)) {}
+    const char* name() const override { return "Dot"; }
+    uint32_t num_inputs() const override { return 2; }
+    matrix& input_at(uint32_t i) override { return i ? bt : a; }
+    void compile(const matrix& out) override {
+        uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+        check(mx_broadcast_shapes_matmul(a.shape(), a.strides(), a.dims, bt.shape(), bt.strides(), bt.dims, os, ost, b1s,
+                                         b1t, b2s, b2t), "broadcast_shapes_matmul");
+        K = a.shape()[a.dims - 1];
+        if (out.dims == 2) {
+            cd = 2;
+            for (int i = 0; i < 2; i++) { cs[i] = os[i]; sA[i] = b1t[i]; sB[i] = b2t[i]; sC[i] = ost[i]; }
+        } else {
+            check(mx_collapse_dims_matmul(os, b1t, b2t, ost, out.dims, kCap, cs, sA, sB, sC, &cd), "collapse_dims_matmul");
+        }
+    }
+    void execute(const matrix& out) override {
+        check(mx_launch_batched_matmul((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a), dptr(bt), nullptr),
+              "launch Dot");
+    }
+    std::vector<matrix> vjp(matrix& g) override {
+        // grad_a = g . Bt ; grad_Bt = g^T . A  (primitives.cpp:5550-5567)
+        matrix ga = g.dot(bt, false);
+        std::vector<size_m> axes(g.dims);
+        std::iota(axes.begin(), axes.end(), 0);
+        std::swap(axes[g.dims - 2], axes[g.dims - 1]);
+        matrix gb = g.transpose(axes).dot(a, false);
+        return {ga.unbroadcast_shape(a.shape(), a.dims), gb.unbroadcast_shape(bt.shape(), bt.dims)};
+    }
+};
+
+// Strided copy with cast into a contiguous output.
+struct CopyPrim : Primitive {
+    matrix in;
+    uint32_t cd = 0;
+    uint32_t cs[MX_MAX_DIMS], sD[MX_MAX_DIMS], sS[MX_MAX_DIMS];
+    explicit CopyPrim(matrix x) : in(std::move(x)) {}
+    const char* name() const override { return "AsType"; }
+    uint32_t num_inputs() const override { return 1; }
+    matrix& input_at(uint32_t) override { return in; }
+    void compile(const matrix& out) override {
+        if (in.dims == 0) { cd = 0; return; }
+        const std::vector<size_m> dst = contiguous_strides(in.shape_vec());
+        check(mx_collapse_dims2(in.shape(), dst.data(), in.strides(), in.dims, kCap, cs, sD, sS, &cd), "collapse_dims");
+        (void)out;
+    }
+    void execute(const matrix& out) override {
+        check(mx_launch_copy_strided((int)out.type, (int)in.type, (int)cd, cs, sD, sS, dptr(out), dptr(in), nullptr),
+              "launch AsType");
+    }
+    std::vector<matrix> vjp(matrix& g) override { return {g.astype(in.type)}; }
+};
+
+// Channels-last convolution.
+struct ConvPrim : Primitive {
+    matrix in, k;
+    std::vector<int> stride, pad_lo, dil, dil_lhs;
+    int groups;
+    bool flip;
+    std::vector<uint32_t> ishape, kshape, oshape, ist, kst, ost;
+    DevBuf ws;
+    size_t ws_bytes = 0;
+    ConvPrim(matrix x, matrix w, std::vector<int> s, std::vector<int> pl, std::vector<int> d, std::vector<int> dl, int g,
+             bool f)
+        : in(std::move(x)), k(std::move(w)), stride(std::move(s)), pad_lo(std::move(pl)), dil(std::move(d)),
+          dil_lhs(std::move(dl)), groups(g), flip(f) {}
+    const char* name() const override { return "Convolve"; }
+    uint32_t num_inputs() const override { return 2; }
+    matrix& input_at(uint32_t i) override { return i ? k : in; }
+    void compile(const matrix& out) override {
+        ishape = in.shape_vec(); kshape = k.shape_vec(); oshape = out.shape_vec();
+        ist = in.strides_vec(); kst = k.strides_vec(); ost = out.strides_vec();
+        check(mx_conv_workspace_bytes((int)in.type, (int)in.dims - 2, ishape.data(), kshape.data(), oshape.data(),
+                                      ist.data(), kst.data(), ost.data(), groups, &ws_bytes), "conv workspace");
+        if (ws_bytes) ws.reserve(ws_bytes);
+    }
+    void execute(const matrix& out) override {
+        check(mx_launch_conv_nd((int)in.type, (int)in.dims - 2, ishape.data(), kshape.data(), oshape.data(), ist.data(),
+                                kst.data(), ost.data(), pad_lo.data(), stride.data(), dil.data(), dil_lhs.data(), groups,
+                                flip ? 1 : 0, dptr(out), dptr(in), dptr(k), ws.p, ws_bytes, nullptr),
+              "launch Convolve");
+    }
+    std::vector<matrix> vjp(matrix&) override { throw std::logic_error("matrix: no vjp for Convolve"); }
+};
+
+// Result dtype of a binary op: equal dtypes pass; a rank-0 operand takes the other's dtype
+// (scalar_operand_type); otherwise the wider of the two, floats before integers.
+dtype common_type(const matrix& a, const matrix& b) {
+    if (a.type == b.type) return a.type;
+    if (a.dims == 0 && b.dims > 0) return b.type;
+    if (b.dims == 0 && a.dims > 0) return a.type;
+    auto rank = [](dtype t) {
+        switch (t) {
+        case dtype::Float: return 100;
+        case dtype::BFloat16: return 91;
+        case dtype::Float16: return 90;
+        case dtype::Int64: case dtype::UInt64: return 60;
+        case dtype::Int32: case dtype::UInt32: return 50;
+        case dtype::Int16: case dtype::UInt16: return 40;
+        default: return 30;
+        }
+    };
+    if ((a.type == dtype::Float16 && b.type == dtype::BFloat16) || (a.type == dtype::BFloat16 && b.type == dtype::Float16))
+        return dtype::Float;
+    return rank(a.type) >= rank(b.type) ? a.type : b.type;
+}
+
+matrix binary(int op, const matrix& x, const matrix& y) {
+    if (!x.storage || !y.storage) throw std::invalid_argument("matrix: operand is empty");
+    const dtype t = common_type(x, y);
+    matrix a = x.type == t ? x : x.astype(t);
+    matrix b = y.type == t ? y : y.astype(t);
+    uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+    if (mx_broadcast_shapes(a.shape(), a.strides(), a.dims, b.shape(), b.strides(), b.dims, os, ost, b1s, b1t, b2s,
+                            b2t) != MX_OK)
+        throw std::invalid_argument(std::string("matrix: ") + mx_last_error());
+    const uint32_t nd = std::max(a.dims, b.dims);
+    std::vector<size_m> shape(os, os + nd);
+    return matrix::make_node(shape, t, std::make_shared<BinaryPrim>(op, a, b));
+}
+
+matrix reduce(int op, const matrix& x, int axis, bool keepdims, const char* who) {
+    if (x.dims == 0) throw std::invalid_argument(std::string("matrix::") + who + ": rank-0 input");
+    axis = norm_axis(axis, x.dims, who);
+    std::vector<size_m> shape;
+    for (uint32_t i = 0; i < x.dims; i++) {
+        if ((int)i == axis) { if (keepdims) shape.push_back(1); }
+        else shape.push_back(x.shape()[i]);
+    }
+    const dtype t = (op == MX_RED_ARGMAX || op == MX_RED_ARGMIN) ? dtype::Int32 : x.type;
+    return matrix::make_node(shape, t, std::make_shared<ReducePrim>(op, x, axis, keepdims));
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ views and casts
+matrix matrix::transpose(const std::vector<size_m>& order) const {
+    if (order.size() != dims) throw std::invalid_argument("matrix::transpose: order must name every axis");
+    std::vector<size_m> s(dims), st(dims);
+    std::vector<bool> seen(dims, false);
+    for (uint32_t i = 0; i < dims; i++) {
+        if (order[i] >= dims || seen[order[i]]) throw std::invalid_argument("matrix::transpose: bad axis order");
+        seen[order[i]] = true;
+        s[i] = shp_[order[i]];
+        st[i] = str_[order[i]];
+    }
+    return make_view(*this, s, st, offset, std::make_shared<ViewPrim>(ViewPrim::Transpose, *this, order));
+}
+
+matrix matrix::reshape(const std::vector<size_m>& new_shape) const {
+    if (prod(new_shape) != prod(shp_)) throw std::invalid_argument("matrix::reshape: element count changes");
+    if (!is_contiguous()) return astype(type, true).reshape(new_shape);
+    return make_view(*this, new_shape, contiguous_strides(new_shape), offset,
+                     std::make_shared<ViewPrim>(ViewPrim::Reshape, *this));
+}
+
+matrix matrix::flatten(int start, int end) const {
+    if (dims == 0) return reshape({1});
+    start = norm_axis(start, dims, "flatten");
+    end = norm_axis(end, dims, "flatten");
+    if (end < start) throw std::invalid_argument("matrix::flatten: end before start");
+    std::vector<size_m> s;
+    for (int i = 0; i < start; i++) s.push_back(shp_[i]);
+    uint64_t m = 1;
+    for (int i = start; i <= end; i++) m *= shp_[i];
+    s.push_back((size_m)m);
+    for (uint32_t i = end + 1; i < dims; i++) s.push_back(shp_[i]);
+    return reshape(s);
+}
+
+matrix matrix::unsqueeze(int axis) const {
+    if (axis < 0) axis += (int)dims + 1;
+    if (axis < 0 || axis > (int)dims) throw std::invalid_argument("matrix::unsqueeze: axis out of range");
+    std::vector<size_m> s = shp_, st = str_;
+    const size_m stride = axis < (int)dims ? str_[axis] * shp_[axis] : 1;
+    s.insert(s.begin() + axis, 1);
+    st.insert(st.begin() + axis, stride);
+    return make_view(*this, s, st, offset, std::make_shared<ViewPrim>(ViewPrim::Reshape, *this));
+}
+
+matrix matrix::broadcast_to(const std::vector<size_m>& shape) const {
+    if (shape.size() < dims) throw std::invalid_argument("matrix::broadcast_to: target rank below source rank");
+    const size_t lead = shape.size() - dims;
+    std::vector<size_m> st(shape.size(), 0);
+    for (uint32_t i = 0; i < dims; i++) {
+        if (shp_[i] == shape[lead + i]) st[lead + i] = str_[i];
+        else if (shp_[i] == 1) st[lead + i] = 0;
+        else throw std::invalid_argument("MatrixH: Incompatible shapes for broadcasting");
+    }
+    return make_view(*this, shape, st, offset, std::make_shared<ViewPrim>(ViewPrim::Broadcast, *this));
+}
+
+matrix matrix::astype(dtype t, bool make_contig) const {
+    if (t == type && (!make_contig || is_contiguous())) return *this;
+    return make_node(shp_, t, std::make_shared<CopyPrim>(*this));
+}
+
+// ------------------------------------------------------------------ ops
+matrix operator+(const matrix& a, const matrix& b) { return binary(MX_OP_ADD, a, b); }
+matrix operator-(const matrix& a, const matrix& b) { return binary(MX_OP_SUB, a, b); }
+matrix operator*(const matrix& a, const matrix& b) { return binary(MX_OP_MUL, a, b); }
+matrix operator/(const matrix& a, const matrix& b) { return binary(MX_OP_DIV, a, b); }
+
+// max / min do not cast (Matrix.mm:13363-13376): the operands must share a dtype, except a
+// rank-0 scalar, which takes the other operand's.
+static void require_same_type(const matrix& a, const matrix& b, const char* who) {
+    if (a.type != b.type && a.dims != 0 && b.dims != 0)
+        throw std::invalid_argument(std::string("matrix::") + who + ": operands must have the same dtype");
+}
+matrix matrix::max(const matrix& a, const matrix& b) { require_same_type(a, b, "max"); return binary(MX_OP_MAX, a, b); }
+matrix matrix::min(const matrix& a, const matrix& b) { require_same_type(a, b, "min"); return binary(MX_OP_MIN, a, b); }
+matrix matrix::equal(const matrix& a, const matrix& b) { return binary(MX_OP_EQ, a, b); }
+
+matrix matrix::sum(int axis, bool keepdims) const { return reduce(MX_RED_SUM, *this, axis, keepdims, "sum"); }
+matrix matrix::sum(int start, int end, bool keepdims) const { return flatten(start, end).sum(start, keepdims); }
+matrix matrix::sum() const { return flatten(0, -1).sum(0); }
+matrix matrix::max(int axis, bool keepdims) const { return reduce(MX_RED_MAX, *this, axis, keepdims, "max"); }
+matrix matrix::min(int axis, bool keepdims) const { return reduce(MX_RED_MIN, *this, axis, keepdims, "min"); }
+matrix matrix::argmax(int axis, bool keepdims) const { return reduce(MX_RED_ARGMAX, *this, axis, keepdims, "argmax"); }
+matrix matrix::argmin(int axis, bool keepdims) const { return reduce(MX_RED_ARGMIN, *this, axis, keepdims, "argmin"); }
+matrix matrix::SumNoRed(int axis) const { return sum(axis, true); }
+
+// Sums the gradient of a broadcast operand back to its shape (Matrix.mm:5425-5443).
+matrix matrix::unbroadcast_shape(const size_m* target_shape, int target_dims) const {
+    matrix result = *this;
+    const int rank_diff = (int)dims - target_dims;
+    if (rank_diff > 0) result = result.sum(0, rank_diff - 1, false);
+    for (int i = 0; i < target_dims; i++)
+        if (target_shape[i] == 1 && result.shape()[i] != 1) result = result.SumNoRed(i);
+    return result;
+}
+
+// dot packs B^T contiguous (and A when it is a strided view) before the product, as the
+// reference does (Matrix.mm:7068-7092).
+matrix matrix::dot(const matrix& b, bool transposeB) const {
+    if (dims < 2 || b.dims < 2) throw std::invalid_argument("matrix::dot requires both matrices to be at least 2D");
+    matrix bt = b;
+    if (!transposeB) {
+        std::vector<size_m> axes(b.dims);
+        std::iota(axes.begin(), axes.end(), 0);
+        std::swap(axes[b.dims - 2], axes[b.dims - 1]);
+        bt = b.transpose(axes);
+    }
+    if (!bt.is_contiguous()) bt = bt.astype(bt.type, true);
+    matrix a = is_contiguous() ? *this : astype(type, true);
+    if (bt.type != a.type) bt = bt.astype(a.type, true);
+    uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+    if (mx_broadcast_shapes_matmul(a.shape(), a.strides(), a.dims, bt.shape(), bt.strides(), bt.dims, os, ost, b1s, b1t,
+                                   b2s, b2t) != MX_OK)
+        throw std::invalid_argument(std::string("matrix::dot: ") + mx_last_error());
+    const uint32_t nd = std::max(a.dims, bt.dims);
+    return make_node(std::vector<size_m>(os, os + nd), a.type, std::make_shared<DotPrim>(a, bt));
+}
+
+// conv (Matrix.mm:12267-12333): output extent (dilated_in + lo + hi - dilated_k) / stride + 1.
+matrix matrix::conv(const matrix& input, const matrix& kernel, const std::vector<int>& stride,
+                    const std::vector<int>& pad_lo, const std::vector<int>& pad_hi,
+                    const std::vector<int>& kernel_dilation, const std::vector<int>& input_dilation, int groups,
+                    bool flip) {
+    if (input.dims < 3 || input.dims != kernel.dims)
+        throw std::invalid_argument("matrix::conv: input and kernel must have the same rank >= 3");
+    const int ns = (int)input.dims - 2;
+    auto chk = [&](const std::vector<int>& v, const char* what) {
+        if ((int)v.size() != ns) throw std::invalid_argument(std::string("matrix::conv: ") + what + " needs one entry per spatial axis");
+    };
+    chk(stride, "stride"); chk(pad_lo, "padding"); chk(pad_hi, "padding"); chk(kernel_dilation, "kernel dilation");
+    chk(input_dilation, "input dilation");
+    if (input.type != kernel.type) throw std::invalid_argument("matrix::conv: input and kernel dtypes differ");
+    if (groups < 1 || input.shape()[ns + 1] % groups || kernel.shape()[0] % groups ||
+        input.shape()[ns + 1] / groups != kernel.shape()[ns + 1])
+        throw std::invalid_argument("matrix::conv: channels do not match the kernel and groups");
+    std::vector<size_m> out = {input.shape()[0]};
+    for (int d = 0; d < ns; d++) {
+        if (stride[d] < 1 || kernel_dilation[d] < 1 || input_dilation[d] < 1)
+            throw std::invalid_argument("matrix::conv: stride and dilations must be >= 1");
+        const int64_t din = ((int64_t)input.shape()[d + 1] - 1) * input_dilation[d] + 1;
+        const int64_t dk = ((int64_t)kernel.shape()[d + 1] - 1) * kernel_dilation[d] + 1;
+        const int64_t span = din + pad_lo[d] + pad_hi[d] - dk;
+        if (span < 0) throw std::invalid_argument("matrix::conv: kernel larger than the padded input");
+        out.push_back((size_m)(span / stride[d] + 1));
+    }
+    out.push_back(kernel.shape()[0]);
+    return make_node(out, input.type, std::make_shared<ConvPrim>(input, kernel, stride, pad_lo, kernel_dilation,
+                                                                 input_dilation, groups, flip));
+}
+
+matrix matrix::conv2d(const matrix& input, const matrix& kernel, int stride_h, int stride_w, int pad_h, int pad_w,
+                      int dilation_h, int dilation_w, int groups, int input_dilation_h, int input_dilation_w,
+                      bool flip) {
+    return conv(input, kernel, {stride_h, stride_w}, {pad_h, pad_w}, {pad_h, pad_w}, {dilation_h, dilation_w},
+                {input_dilation_h, input_dilation_w}, groups, flip);
+}
+
+// ------------------------------------------------------------------ compile / execute
+namespace {
+
+void compile_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {
+    if (!m.storage) throw std::invalid_argument("matrix: empty handle in the graph");
+    if (!m.tape) {                                  // leaf: device copy of the host values
+        if (!m.storage->dev || m.storage->dev_stale) m.storage->upload();
+        return;
+    }
+    if (!seen.insert(m.tape.get()).second) return;
+    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) compile_node(m.tape->input_at(i), seen);
+    if (!m.tape->compiled) {
+        if (!m.tape->is_view()) m.storage->allocate();
+        m.tape->compile(m);
+        m.tape->compiled = true;
+    }
+}
+
+void execute_node(const matrix& m) {
+    if (!m.tape) {
+        if (m.storage->dev_stale) m.storage->upload();      // leaf written on the host
+        return;
+    }
+    if (m.tape->evaluated) return;
+    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) execute_node(m.tape->input_at(i));
+    if (!m.tape->compiled) throw std::logic_error("matrix: execute before compile");
+    m.tape->execute(m);
+    m.tape->evaluated = true;
+}
+
+void clear_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {
+    if (!m.tape || !seen.insert(m.tape.get()).second) return;
+    m.tape->evaluated = false;
+    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) clear_node(m.tape->input_at(i), seen);
+}
+
+}  // namespace
+
+void matrix::compile_gpu(std::vector<matrix>& ms) {
+    matrix_amd::init();
+    std::unordered_set<const Primitive*> seen;
+    for (auto& m : ms) compile_node(m, seen);
+}
+void matrix::execute_gpu(std::vector<matrix>& ms) {
+    for (auto& m : ms) execute_node(m);
+    check(mx_hip_sync(nullptr), "execute");
+}
+void matrix::clear_trace_checks(std::vector<matrix>& ms) {
+    std::unordered_set<const Primitive*> seen;
+    for (auto& m : ms) clear_node(m, seen);
+}
+void matrix::eval(std::vector<matrix>& ms) {
+    compile_gpu(ms);
+    execute_gpu(ms);
+}
+void matrix::compile_gpu() { std::vector<matrix> v{*this}; compile_gpu(v); }
+void matrix::execute_gpu() { std::vector<matrix> v{*this}; execute_gpu(v); }
+void matrix::clear_trace_checks() { std::vector<matrix> v{*this}; clear_trace_checks(v); }
+void matrix::eval() { std::vector<matrix> v{*this}; eval(v); }
+
+std::vector<uint8_t> matrix::to_host_bytes() const {
+    const size_t es = dtype_size(type);
+    std::vector<uint8_t> full;
+    if (tape) {
+        if (!tape->evaluated) { matrix self = *this; self.eval(); }
+        full.resize(storage->bytes);
+        if (storage->bytes) check(mx_hip_d2h(full.data(), storage->dev, storage->bytes, nullptr), "device-to-host copy");
+    } else {
+        full = storage->host;
+    }
+    const size_t n = total_size();
+    std::vector<uint8_t> out(n * es);
+    std::vector<size_m> idx(dims, 0);
+    for (size_t i = 0; i < n; i++) {
+        uint64_t off = offset;
+        for (uint32_t d = 0; d < dims; d++) off += (uint64_t)idx[d] * str_[d];
+        std::memcpy(out.data() + i * es, full.data() + off * es, es);
+        for (int d = (int)dims - 1; d >= 0; --d) {
+            if (++idx[d] < shp_[d]) break;
+            idx[d] = 0;
+        }
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ autodiff (Matrix.mm:1327-1411)
+namespace {
+const void* node_id(const matrix& m) { return m.tape ? (const void*)m.tape.get() : (const void*)m.storage.get(); }
+}  // namespace
+
+std::vector<matrix> matrix::build_grad_graph(std::vector<matrix>& output_nodes, std::vector<matrix>& sample_input_nodes) {
+    std::vector<const matrix*> topo;
+    std::unordered_map<const void*, bool> depends;
+    std::unordered_map<const void*, matrix> grads;
+    std::unordered_set<const void*> params;
+    for (auto& p : sample_input_nodes) params.insert(node_id(p));
+
+    std::function<void(const matrix&)> dfs = [&](const matrix& m) {
+        const void* id = node_id(m);
+        if (depends.count(id)) return;
+        bool dep = false;
+        if (m.tape) {
+            for (uint32_t i = 0; i < m.tape->num_inputs(); i++) {
+                const matrix& in = m.tape->input_at(i);
+                dfs(in);
+                if (depends[node_id(in)]) dep = true;
+            }
+        }
+        depends[id] = params.count(id) || dep;
+        topo.push_back(&m);
+    };
+    for (auto& out : output_nodes) {
+        dfs(out);
+        if (depends[node_id(out)]) grads.insert({node_id(out), out.ones()});
+    }
+    for (auto it = topo.rbegin(); it != topo.rend(); ++it) {
+        const matrix& m = **it;
+        if (!m.tape || !depends[node_id(m)]) continue;
+        auto g = grads.find(node_id(m));
+        if (g == grads.end()) continue;
+        matrix current = g->second;
+        std::vector<matrix> in_grads = m.tape->vjp(current);
+        const uint32_t n = m.tape->num_inputs();
+        if (in_grads.size() != n)
+            throw std::logic_error("matrix: build_grad_graph => a vjp returned " + std::to_string(in_grads.size()) +
+                                   " gradients for " + std::to_string(n) + " inputs");
+        for (uint32_t i = 0; i < n; i++) {
+            const void* in_id = node_id(m.tape->input_at(i));
+            if (!depends[in_id]) continue;
+            auto f = grads.find(in_id);
+            if (f != grads.end()) f->second = f->second + in_grads[i];
+            else grads.insert({in_id, in_grads[i]});
+        }
+    }
+    std::vector<matrix> out;
+    for (auto& p : sample_input_nodes) {
+        auto f = grads.find(node_id(p));
+        out.push_back(f != grads.end() ? f->second : p.zeros());
+    }
+    return out;
+}
+
+matrix matrix::build_grad_graph(matrix& output_node, matrix& sample_input_node) {
+    std::vector<matrix> o{output_node}, p{sample_input_node};
+    return build_grad_graph(o, p)[0];
+}
+
+std::function<std::pair<matrix, std::vector<matrix>>(const std::vector<matrix>&)> matrix::value_and_grad(
+    std::function<matrix(std::vector<matrix>)> fn) {
+    return [fn](const std::vector<matrix>& params) {
+        std::vector<matrix> ps = params;
+        matrix value = fn(ps);
+        if (value.total_size() != 1)     // like MLX: a gradient needs a single-element output
+            throw std::invalid_argument("matrix::value_and_grad: the function must return a single element");
+        std::vector<matrix> outs{value};
+        std::vector<matrix> grads = build_grad_graph(outs, ps);
+        std::vector<matrix> all = grads;
+        all.push_back(value);
+        eval(all);
+        return std::make_pair(value, grads);
+    };
+}
+
+std::function<std::vector<matrix>(const std::vector<matrix>&)> matrix::grad(std::function<matrix(std::vector<matrix>)> fn) {
+    auto vg = value_and_grad(std::move(fn));
+    return [vg](const std::vector<matrix>& params) { return vg(params).second; };
+}

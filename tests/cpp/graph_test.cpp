@@ -1,0 +1,380 @@
+// graph_test.cpp -- tests of the lazy-graph layer (matrix_amd/host/matrix.hpp).
+//
+//   graph_test cpu   graph building only (shape inference, errors, gradient-graph structure);
+//                    touches no device
+//   graph_test gpu   graphs evaluated on the GPU against double-precision host loops of the
+//                    same mathematics (independent of the kernels and of the oracle)
+//
+// Prints "PASS <name>" / "FAIL <name>: <why>" per case; exit status 1 if any case failed.
+#include "../../matrix_amd/host/matrix.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <random>
+#include <string>
+#include <vector>
+
+static int g_fail = 0;
+
+#define CASE(name) static void name()
+#define EXPECT(cond, msg)                                                     \
+    do {                                                                      \
+        if (!(cond)) throw std::runtime_error(std::string(msg));              \
+    } while (0)
+
+static void run(const char* name, void (*fn)()) {
+    try {
+        fn();
+        std::printf("PASS %s\n", name);
+    } catch (const std::exception& e) {
+        std::printf("FAIL %s: %s\n", name, e.what());
+        g_fail++;
+    }
+    std::fflush(stdout);
+}
+
+template <typename F>
+static bool throws(F&& f) {
+    try { f(); } catch (const std::invalid_argument&) { return true; }
+    return false;
+}
+
+static std::vector<float> randn(size_t n, uint64_t seed, float scale = 1.0f) {
+    std::mt19937_64 g(seed);
+    std::normal_distribution<float> d(0.0f, 1.0f);
+    std::vector<float> v(n);
+    for (auto& x : v) x = d(g) * scale;
+    return v;
+}
+static std::vector<float> randu(size_t n, uint64_t seed, float lo, float hi) {
+    std::mt19937_64 g(seed);
+    std::uniform_real_distribution<float> d(lo, hi);
+    std::vector<float> v(n);
+    for (auto& x : v) x = d(g);
+    return v;
+}
+
+static double rel_err(const std::vector<float>& got, const std::vector<double>& ref) {
+    double num = 0, den = 0;
+    for (size_t i = 0; i < ref.size(); i++) {
+        num += (got[i] - ref[i]) * (got[i] - ref[i]);
+        den += ref[i] * ref[i];
+    }
+    return std::sqrt(num / (den > 0 ? den : 1));
+}
+
+// ------------------------------------------------------------------ CPU (build-only) cases
+CASE(shapes_broadcast_and_reduce) {
+    matrix a = matrix::leaf({4096, 1024});
+    matrix b = matrix::leaf({1, 1024});
+    matrix c = a + b;
+    EXPECT(c.dims == 2 && c.shape()[0] == 4096 && c.shape()[1] == 1024, "broadcast shape");
+    matrix s = c.sum(1);
+    EXPECT(s.dims == 1 && s.shape()[0] == 4096, "sum(1) shape");
+    EXPECT(c.sum(1, true).dims == 2 && c.sum(1, true).shape()[1] == 1, "keepdims shape");
+    matrix g = c.sum();
+    EXPECT(g.dims == 0 && g.total_size() == 1, "global sum is rank 0");
+    EXPECT(c.argmax(0).type == dtype::Int32 && c.argmax(0).shape()[0] == 1024, "argmax dtype / shape");
+    EXPECT(throws([&] { (void)(matrix::leaf({3, 4}) + matrix::leaf({5, 4})); }), "incompatible broadcast throws");
+    EXPECT(throws([&] { (void)a.sum(2); }), "axis out of range throws");
+}
+
+CASE(shapes_dot_and_conv) {
+    matrix a = matrix::leaf({16, 64, 32});
+    matrix b = matrix::leaf({32, 48});
+    matrix c = a.dot(b);
+    EXPECT(c.dims == 3 && c.shape()[0] == 16 && c.shape()[1] == 64 && c.shape()[2] == 48, "dot shape");
+    EXPECT(throws([&] { (void)a.dot(matrix::leaf({31, 48})); }), "core-dimension mismatch throws");
+    matrix x = matrix::leaf({2, 56, 56, 64});
+    matrix w = matrix::leaf({128, 3, 3, 64});
+    matrix y = matrix::conv2d(x, w, 1, 1, 1, 1);
+    EXPECT(y.shape()[0] == 2 && y.shape()[1] == 56 && y.shape()[2] == 56 && y.shape()[3] == 128, "conv2d shape");
+    matrix y2 = matrix::conv2d(x, matrix::leaf({32, 1, 1, 64}), 2, 2);
+    EXPECT(y2.shape()[1] == 28 && y2.shape()[2] == 28, "strided 1x1 shape");
+    EXPECT(throws([&] { (void)matrix::conv2d(x, matrix::leaf({8, 3, 3, 60})); }), "channel mismatch throws");
+}
+
+CASE(views_share_storage) {
+    matrix a = matrix::leaf({3, 4, 5});
+    matrix t = a.transpose({2, 0, 1});
+    EXPECT(t.storage == a.storage && t.shape()[0] == 5 && t.strides()[0] == 1 && !t.is_contiguous(), "transpose view");
+    matrix r = a.reshape({12, 5});
+    EXPECT(r.storage == a.storage && r.is_contiguous(), "reshape of contiguous is a view");
+    matrix rt = t.reshape({5, 12});
+    EXPECT(rt.storage != a.storage, "reshape of a strided view copies");
+    matrix bb = matrix::leaf({1, 5}).broadcast_to({4, 5});
+    EXPECT(bb.strides()[0] == 0, "broadcast stride 0");
+}
+
+CASE(grad_graph_structure) {
+    matrix x = matrix::leaf({8, 16});
+    matrix w = matrix::leaf({16, 4});
+    matrix b = matrix::leaf({4});
+    matrix y = matrix::max(x.dot(w) + b, matrix::scalar(0.0f));
+    matrix loss = (y * y).sum();
+    std::vector<matrix> outs{loss}, params{w, b};
+    std::vector<matrix> g = matrix::build_grad_graph(outs, params);
+    EXPECT(g.size() == 2, "two gradients");
+    EXPECT(g[0].dims == 2 && g[0].shape()[0] == 16 && g[0].shape()[1] == 4, "dW shape");
+    EXPECT(g[1].dims == 1 && g[1].shape()[0] == 4, "db shape (unbroadcast)");
+    matrix unused = matrix::leaf({3});
+    std::vector<matrix> p2{unused};
+    std::vector<matrix> g2 = matrix::build_grad_graph(outs, p2);
+    EXPECT(g2[0].tape == nullptr && g2[0].shape()[0] == 3, "unused parameter gets zeros");
+    EXPECT(throws([&] { (void)matrix::value_and_grad([](std::vector<matrix> p) { return p[0] * 2.0f; })({matrix::leaf({3})}); }),
+           "value_and_grad needs a single-element output");
+}
+
+// ------------------------------------------------------------------ GPU cases
+CASE(gpu_add_then_rowsum) {
+    const size_m R = 4096, Cc = 1024;
+    auto av = randn((size_t)R * Cc, 0);
+    auto bv = randu(Cc, 1, -1.f, 1.f);
+    matrix a = matrix::from_host<float>({R, Cc}, av);
+    matrix b = matrix::from_host<float>({1, Cc}, bv);
+    matrix c = a + b;
+    matrix s = c.sum(1);
+    std::vector<matrix> outs{c, s};
+    matrix::eval(outs);
+    auto cg = c.to_host<float>();
+    auto sg = s.to_host<float>();
+    for (size_t i = 0; i < (size_t)R * Cc; i++)
+        EXPECT(cg[i] == av[i] + bv[i % Cc], "add is not exact");
+    for (size_t r = 0; r < R; r++) {
+        double ref = 0, mag = 0;
+        for (size_t j = 0; j < Cc; j++) { ref += (double)cg[r * Cc + j]; mag += std::fabs(cg[r * Cc + j]); }
+        EXPECT(std::fabs(sg[r] - ref) <= 1e-4 * mag, "row sum beyond 1e-4 of sum|x|");
+    }
+}
+
+CASE(gpu_reductions_and_views) {
+    const size_m R = 64, Cc = 4 * 256 * 16;
+    auto xv = randn((size_t)R * Cc, 2);
+    matrix x = matrix::from_host<float>({R, Cc}, xv);
+    matrix mx0 = x.max(0), mn1 = x.min(1), am1 = x.argmax(1), an0 = x.argmin(0);
+    matrix chain = x.reshape({16, 4, 256, 64}).sum(3).sum(1);     // reduce a strided split
+    matrix tsum = x.transpose({1, 0}).sum(1);                      // reduce over a transposed view
+    std::vector<matrix> outs{mx0, mn1, am1, an0, chain, tsum};
+    matrix::eval(outs);
+    auto a0 = mx0.to_host<float>(), a1 = mn1.to_host<float>(), t1 = tsum.to_host<float>(), ch = chain.to_host<float>();
+    auto i1 = am1.to_host<int32_t>(), i0 = an0.to_host<int32_t>();
+    for (size_t j = 0; j < Cc; j++) {
+        float m = -3.4028234663852886e38f, mn = 3.4028234663852886e38f;
+        int32_t im = 0;
+        double s = 0;
+        for (size_t r = 0; r < R; r++) {
+            const float v = xv[r * Cc + j];
+            if (m < v) m = v;
+            if (v < mn) { mn = v; im = (int32_t)r; }
+            s += v;
+        }
+        EXPECT(a0[j] == m, "max(0)");
+        EXPECT(i0[j] == im, "argmin(0)");
+        EXPECT(std::fabs(t1[j] - s) <= 1e-4 * R * 4, "sum over transposed view");
+    }
+    for (size_t r = 0; r < R; r++) {
+        float mn = 3.4028234663852886e38f, mx = -3.4028234663852886e38f;
+        int32_t im = 0;
+        for (size_t j = 0; j < Cc; j++) {
+            const float v = xv[r * Cc + j];
+            if (v < mn) mn = v;
+            if (v > mx) { mx = v; im = (int32_t)j; }
+        }
+        EXPECT(a1[r] == mn, "min(1)");
+        EXPECT(i1[r] == im, "argmax(1)");
+    }
+    // chain: [16,4,256,64] summed over axes 3 then 1 -> [16,256]
+    for (size_t a = 0; a < 16; a++)
+        for (size_t c = 0; c < 256; c++) {
+            double s = 0, mag = 0;
+            for (size_t b = 0; b < 4; b++)
+                for (size_t d = 0; d < 64; d++) {
+                    const float v = xv[((a * 4 + b) * 256 + c) * 64 + d];
+                    s += v;
+                    mag += std::fabs(v);
+                }
+            EXPECT(std::fabs(ch[a * 256 + c] - s) <= 1e-4 * mag, "sum(3).sum(1) chain");
+        }
+}
+
+CASE(gpu_dot_batched_broadcast) {
+    const size_m B = 4, M = 200, K = 300, N = 150;
+    auto av = randn((size_t)B * M * K, 3, 1.0f / std::sqrt((float)K));
+    auto bv = randn((size_t)K * N, 4);
+    matrix a = matrix::from_host<float>({B, M, K}, av);
+    matrix b = matrix::from_host<float>({K, N}, bv);
+    matrix c = a.dot(b);
+    auto cg = c.to_host<float>();
+    std::vector<double> ref((size_t)B * M * N, 0.0);
+    for (size_t bb = 0; bb < B; bb++)
+        for (size_t m = 0; m < M; m++)
+            for (size_t k = 0; k < K; k++) {
+                const double x = av[(bb * M + m) * K + k];
+                for (size_t n = 0; n < N; n++) ref[(bb * M + m) * N + n] += x * bv[k * N + n];
+            }
+    EXPECT(rel_err(cg, ref) <= 1e-4, "dot normwise error above 1e-4");
+}
+
+CASE(gpu_conv2d_nchw_views) {
+    const size_m N = 2, C = 16, H = 9, W = 8, O = 12;
+    auto xv = randn((size_t)N * C * H * W, 5);
+    auto wv = randn((size_t)O * C * 9, 6, 0.2f);
+    matrix x = matrix::from_host<float>({N, C, H, W}, xv).transpose({0, 2, 3, 1});   // NHWC view
+    matrix w = matrix::from_host<float>({O, C, 3, 3}, wv).transpose({0, 2, 3, 1});   // OHWI view
+    matrix y = matrix::conv2d(x, w, 1, 1, 1, 1);
+    auto yg = y.to_host<float>();
+    std::vector<double> ref((size_t)N * H * W * O, 0.0);
+    for (size_t n = 0; n < N; n++)
+        for (size_t oh = 0; oh < H; oh++)
+            for (size_t ow = 0; ow < W; ow++)
+                for (size_t o = 0; o < O; o++) {
+                    double s = 0;
+                    for (int kh = 0; kh < 3; kh++)
+                        for (int kw = 0; kw < 3; kw++) {
+                            const int ih = (int)oh - 1 + kh, iw = (int)ow - 1 + kw;
+                            if (ih < 0 || iw < 0 || ih >= (int)H || iw >= (int)W) continue;
+                            for (size_t c = 0; c < C; c++)
+                                s += (double)xv[((n * C + c) * H + ih) * W + iw] * wv[((o * C + c) * 3 + kh) * 3 + kw];
+                        }
+                    ref[((n * H + oh) * W + ow) * O + o] = s;
+                }
+    EXPECT(rel_err(yg, ref) <= 1e-4, "conv2d normwise error above 1e-4");
+}
+
+// A small MLP training step: forward loss and every parameter gradient against a
+// double-precision host forward / backward of the same network.
+struct HostMLP {
+    size_m B, D0, D1, D2, D3;
+};
+
+static void host_mlp(const HostMLP& s, const std::vector<float>& x, const std::vector<float>& t,
+                     const std::vector<std::vector<float>>& W, const std::vector<std::vector<float>>& b, double& loss,
+                     std::vector<std::vector<double>>& dW, std::vector<std::vector<double>>& db) {
+    const size_m dimsv[4] = {s.D0, s.D1, s.D2, s.D3};
+    std::vector<std::vector<double>> act(4), pre(4);
+    act[0].assign(x.begin(), x.end());
+    for (int l = 0; l < 3; l++) {
+        const size_m din = dimsv[l], dout = dimsv[l + 1];
+        pre[l + 1].assign((size_t)s.B * dout, 0.0);
+        for (size_t i = 0; i < s.B; i++)
+            for (size_t k = 0; k < din; k++) {
+                const double a = act[l][i * din + k];
+                for (size_t j = 0; j < dout; j++) pre[l + 1][i * dout + j] += a * W[l][k * dout + j];
+            }
+        act[l + 1].resize(pre[l + 1].size());
+        for (size_t i = 0; i < s.B; i++)
+            for (size_t j = 0; j < dout; j++) {
+                const double v = pre[l + 1][i * dout + j] + b[l][j];
+                pre[l + 1][i * dout + j] = v;
+                act[l + 1][i * dout + j] = l < 2 ? (v > 0 ? v : 0) : v;
+            }
+    }
+    loss = 0;
+    std::vector<double> g((size_t)s.B * s.D3);
+    for (size_t i = 0; i < g.size(); i++) {
+        const double d = act[3][i] - t[i];
+        loss += d * d;
+        g[i] = 2 * d;
+    }
+    dW.assign(3, {});
+    db.assign(3, {});
+    for (int l = 2; l >= 0; --l) {
+        const size_m din = dimsv[l], dout = dimsv[l + 1];
+        if (l < 2)
+            for (size_t i = 0; i < g.size(); i++) g[i] = pre[l + 1][i] > 0 ? g[i] : 0.0;   // ReLU (tie at 0 -> 0)
+        dW[l].assign((size_t)din * dout, 0.0);
+        db[l].assign(dout, 0.0);
+        for (size_t i = 0; i < s.B; i++)
+            for (size_t j = 0; j < dout; j++) {
+                const double gv = g[i * dout + j];
+                db[l][j] += gv;
+                for (size_t k = 0; k < din; k++) dW[l][k * dout + j] += act[l][i * din + k] * gv;
+            }
+        std::vector<double> gin((size_t)s.B * din, 0.0);
+        for (size_t i = 0; i < s.B; i++)
+            for (size_t k = 0; k < din; k++) {
+                double acc = 0;
+                for (size_t j = 0; j < dout; j++) acc += g[i * dout + j] * W[l][k * dout + j];
+                gin[i * din + k] = acc;
+            }
+        g.swap(gin);
+    }
+}
+
+CASE(gpu_mlp_training_step_compile_once) {
+    const HostMLP s{32, 64, 96, 80, 10};
+    const size_m dimsv[4] = {s.D0, s.D1, s.D2, s.D3};
+    auto xv = randn((size_t)s.B * s.D0, 7);
+    auto tv = randu((size_t)s.B * s.D3, 8, 0.f, 1.f);
+    std::vector<std::vector<float>> Wv(3), bv(3);
+    for (int l = 0; l < 3; l++) {
+        Wv[l] = randn((size_t)dimsv[l] * dimsv[l + 1], 10 + l, 1.0f / std::sqrt((float)dimsv[l]));
+        bv[l] = randn(dimsv[l + 1], 20 + l, 0.1f);
+    }
+    matrix x = matrix::from_host<float>({s.B, s.D0}, xv);
+    matrix t = matrix::from_host<float>({s.B, s.D3}, tv);
+    std::vector<matrix> params;
+    for (int l = 0; l < 3; l++) {
+        params.push_back(matrix::from_host<float>({dimsv[l], dimsv[l + 1]}, Wv[l]));
+        params.push_back(matrix::from_host<float>({dimsv[l + 1]}, bv[l]));
+    }
+    matrix h1 = matrix::max(x.dot(params[0]) + params[1], matrix::scalar(0.0f));
+    matrix h2 = matrix::max(h1.dot(params[2]) + params[3], matrix::scalar(0.0f));
+    matrix y = h2.dot(params[4]) + params[5];
+    matrix loss = ((y - t) * (y - t)).sum();
+    std::vector<matrix> outs{loss};
+    std::vector<matrix> grads = matrix::build_grad_graph(outs, params);
+    std::vector<matrix> all = grads;
+    all.push_back(loss);
+    matrix::compile_gpu(all);
+    for (int iter = 0; iter < 3; iter++) {
+        if (iter == 2) {           // new inputs through the compiled graph: host write + mark_changed
+            auto x2 = randn((size_t)s.B * s.D0, 99);
+            std::memcpy(x.host_data(), x2.data(), x2.size() * 4);
+            x.mark_changed();
+            xv = x2;
+        }
+        matrix::execute_gpu(all);
+        double lref;
+        std::vector<std::vector<double>> dW, db;
+        host_mlp(s, xv, tv, Wv, bv, lref, dW, db);
+        const float lg = loss.to_host<float>()[0];
+        EXPECT(std::fabs(lg - lref) <= 1e-4 * std::fabs(lref), "loss mismatch");
+        for (int l = 0; l < 3; l++) {
+            EXPECT(rel_err(grads[2 * l].to_host<float>(), dW[l]) <= 1e-4, "dW mismatch, layer " + std::to_string(l));
+            EXPECT(rel_err(grads[2 * l + 1].to_host<float>(), db[l]) <= 1e-4, "db mismatch, layer " + std::to_string(l));
+        }
+        matrix::clear_trace_checks(all);
+    }
+}
+
+CASE(gpu_value_and_grad) {
+    auto xv = randn(100, 30);
+    matrix x = matrix::from_host<float>({100}, xv);
+    auto [val, g] = matrix::value_and_grad([](std::vector<matrix> p) { return (p[0] * p[0] * 3.0f).sum(); })({x});
+    double ref = 0;
+    for (float v : xv) ref += 3.0 * v * v;
+    EXPECT(std::fabs(val.to_host<float>()[0] - ref) <= 1e-4 * ref, "value");
+    auto gv = g[0].to_host<float>();
+    std::vector<double> gref(xv.size());
+    for (size_t i = 0; i < xv.size(); i++) gref[i] = 6.0 * xv[i];
+    EXPECT(rel_err(gv, gref) <= 1e-6, "gradient of 3 x^2");
+}
+
+int main(int argc, char** argv) {
+    const std::string mode = argc > 1 ? argv[1] : "cpu";
+    if (mode == "cpu") {
+        run("shapes_broadcast_and_reduce", shapes_broadcast_and_reduce);
+        run("shapes_dot_and_conv", shapes_dot_and_conv);
+        run("views_share_storage", views_share_storage);
+        run("grad_graph_structure", grad_graph_structure);
+    } else {
+        run("gpu_add_then_rowsum", gpu_add_then_rowsum);
+        run("gpu_reductions_and_views", gpu_reductions_and_views);
+        run("gpu_dot_batched_broadcast", gpu_dot_batched_broadcast);
+        run("gpu_conv2d_nchw_views", gpu_conv2d_nchw_views);
+        run("gpu_mlp_training_step_compile_once", gpu_mlp_training_step_compile_once);
+        run("gpu_value_and_grad", gpu_value_and_grad);
+    }
+    return g_fail ? 1 : 0;
+}
