@@ -78,8 +78,6 @@ class Prepared:
         self.bytes = self.in_bytes + self.out_bytes
         self.ws = mx.reduce_workspace_bytes(op, mx.FLOAT32, self.rs, self.n, self.desc)
         self.W = mx.DeviceBuffer(self.ws) if self.ws else None
-        if self.W:
-            self.W.fill_bytes(0)      # arrival counters start at zero; launches leave them zero
         self.O = mx.DeviceBuffer(self.out_bytes)
 
     def launch(self, mx, in_ptr):
@@ -141,9 +139,151 @@ def run_gpu(args):
     }
 
 
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "f16": 2500.0}
+
+
+def _timed(mx, fn, reps):
+    """Average ms per call of fn over reps back-to-back calls (HIP events on the launch stream)."""
+    fn()
+    mx.sync()
+    e0, e1 = mx.Event(), mx.Event()
+    e0.record()
+    for i in range(reps):
+        fn(i)
+    e1.record()
+    mx.sync()
+    return e0.elapsed_ms(e1) / reps
+
+
+def _normal(rng, shape, scale, dt):
+    x = (rng.standard_normal(shape, dtype=np.float32) * np.float32(scale))
+    return x.astype(np.float16) if dt == "f16" else x
+
+
+def config_add_rowsum(mx):
+    """Config 1: C = A[4096,1024] + B[1,1024] (broadcast), s = C.sum(1); 20 rotated copies of A
+    (320 MiB, more than the Infinity Cache)."""
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal([4096, 1024], dtype=np.float32)
+    b = rng.uniform(-1, 1, [1, 1024]).astype(np.float32)
+    A = [mx.DeviceBuffer.from_numpy(a) for _ in range(20)]
+    B = mx.DeviceBuffer.from_numpy(b)
+    C = [mx.DeviceBuffer(a.nbytes) for _ in range(2)]
+    S = mx.DeviceBuffer(4096 * 4)
+    out, out_st, _, b1st, _, b2st = mx.broadcast_shapes([4096, 1024], [1024, 1], [1, 1024], [1024, 1])
+    desc = mx.collapse_dims3(out, b1st, b2st, out_st)
+    rdesc = mx.collapse_dims_reduce2([4096, 1024], [1], [1024, 1], 1)
+
+    def graph(i=0):
+        c = C[i % 2]
+        mx.launch_bcast_binary(mx.OP_ADD, mx.FLOAT32, desc, c.ptr, A[i % 20].ptr, B.ptr)
+        mx.launch_reduce(mx.RED_SUM, mx.FLOAT32, 1, 1024, rdesc, S.ptr, c.ptr)
+
+    ms = _timed(mx, graph, 40)
+    nbytes = 50_352_128
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+            "bytes": nbytes, "note": "two kernels: broadcast add, row sum"}
+
+
+def config_matmul(mx):
+    """Config 3: A[16,2048,2048] x B[2048,2048] (B broadcast over the batch), f32 and f16 with
+    fp32 accumulation; skinny A[8,1,4096] x B[4096,4096].  B^T is packed once (dot's copy) and
+    the timed launches are the batched-matmul kernel alone."""
+    rng = np.random.default_rng(1)
+    res = {}
+    for dt in ("f32", "f16"):
+        code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
+        a = _normal(rng, [16, 2048, 2048], 1 / np.sqrt(2048), dt)
+        bt = _normal(rng, [2048, 2048], 1 / np.sqrt(2048), dt)
+        A, Bt = mx.DeviceBuffer.from_numpy(a), mx.DeviceBuffer.from_numpy(bt)
+        C = mx.DeviceBuffer(16 * 2048 * 2048 * a.itemsize)
+        desc = ([16, 2048, 2048], [2048 * 2048, 2048, 1], [0, 2048, 1], [2048 * 2048, 2048, 1])
+        ms = _timed(mx, lambda i=0: mx.launch_batched_matmul(code, desc, 2048, C.ptr, A.ptr, Bt.ptr),
+                    5 if dt == "f32" else 20)
+        tf = 274_877_906_944 / (ms * 1e-3) / 1e12
+        res[f"main_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                             "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)}
+        del A, Bt, C
+        # skinny: 8 copies of B rotated (256 MiB and more), bytes = A + B + C
+        a = _normal(rng, [8, 1, 4096], 1 / 64, dt)
+        bt = _normal(rng, [4096, 4096], 1 / 64, dt)
+        A = mx.DeviceBuffer.from_numpy(a)
+        Bs = [mx.DeviceBuffer.from_numpy(bt) for _ in range(8 if dt == "f32" else 12)]
+        C = mx.DeviceBuffer(8 * 4096 * a.itemsize)
+        desc = ([8, 1, 4096], [4096, 4096, 1], [0, 4096, 1], [4096, 4096, 1])
+        ms = _timed(mx, lambda i=0: mx.launch_batched_matmul(code, desc, 4096, C.ptr, A.ptr, Bs[i % len(Bs)].ptr), 40)
+        nbytes = (a.size + bt.size + 8 * 4096) * a.itemsize
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[f"skinny_{dt}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del A, Bs, C
+    return res
+
+
+def config_conv(mx):
+    """Config 4: x [32,64,56,56] (NCHW) * w [128,64,3,3], stride 1, pad 1, fed as the reference's
+    conv2d sees them (NHWC / OHWI transposed views: packing is part of the timed call) and
+    natively channels-last; 1x1 stride 2: x [32,256,28,28] * w [512,256,1,1]."""
+    rng = np.random.default_rng(2)
+
+    def cs(shape):
+        st, acc = [0] * len(shape), 1
+        for i in range(len(shape) - 1, -1, -1):
+            st[i] = acc
+            acc *= shape[i]
+        return st
+
+    res = {}
+    for dt in ("f32", "f16"):
+        code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
+        for name, (n, c, h, w, o, k, pad, stride), layouts in (
+                ("3x3", (32, 64, 56, 56, 128, 3, 1, 1), ("nchw", "nhwc")),
+                ("1x1s2", (32, 256, 28, 28, 512, 1, 0, 2), ("nchw",))):
+            oh = (h + 2 * pad - k) // stride + 1
+            ow = (w + 2 * pad - k) // stride + 1
+            x = _normal(rng, [n, c, h, w], 1.0, dt)
+            wt = _normal(rng, [o, c, k, k], np.sqrt(2.0 / (c * k * k)), dt)
+            X, W = mx.DeviceBuffer.from_numpy(x), mx.DeviceBuffer.from_numpy(wt)
+            Y = mx.DeviceBuffer(n * oh * ow * o * x.itemsize)
+            for layout in layouts:
+                if layout == "nchw":
+                    st = cs([n, c, h, w])
+                    in_st = [st[0], st[2], st[3], st[1]]
+                    kst = cs([o, c, k, k])
+                    k_st = [kst[0], kst[2], kst[3], kst[1]]
+                else:
+                    in_st, k_st = cs([n, h, w, c]), cs([o, k, k, c])
+                geom = dict(in_shape=[n, h, w, c], k_shape=[o, k, k, c], out_shape=[n, oh, ow, o], in_strides=in_st,
+                            k_strides=k_st, out_strides=cs([n, oh, ow, o]), pad=[pad, pad], stride=[stride, stride])
+                wsb = mx.conv_workspace_bytes(code, geom)
+                WS = mx.DeviceBuffer(max(wsb, 256))
+                ms = _timed(mx, lambda i=0: mx.launch_conv_nd(code, geom, Y.ptr, X.ptr, W.ptr, WS.ptr, wsb), 20)
+                flop = 2.0 * n * oh * ow * o * c * k * k
+                tf = flop / (ms * 1e-3) / 1e12
+                res[f"{name}_{layout}_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                                                "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)}
+                del WS
+            del X, W, Y
+    return res
+
+
+def config_mlp():
+    """Config 5: the compiled-graph MLP training step through the C++ graph API (a child process)."""
+    import subprocess
+    exe = os.path.join(ROOT, "matrix_amd", "_bin", "mlp_step")
+    if not os.path.exists(exe):
+        return {"error": "matrix_amd/_bin/mlp_step not built"}
+    out = subprocess.run([exe, "--steps", "30", "--warmup", "5"], capture_output=True, text=True, timeout=300)
+    if out.returncode != 0:
+        return {"error": (out.stderr or out.stdout).strip()[-300:]}
+    r = json.loads(out.stdout.strip().splitlines()[-1])
+    r["frac_mfma"] = round(r["tflops"] / MFMA_PEAK_TFLOPS["f32"], 4)
+    return r
+
+
 def run_cpu_baseline(mx_collapse):
     """The oracle (the reference's CPU loops restated) single-threaded on the host: the whole
-    step's ops on the same X, repeated until about 5 s of CPU time; GB/s of algorithmic bytes."""
+    step's ops on the same X, repeated until about 10 s of CPU time; GB/s of algorithmic bytes."""
     from oracle import oracle as orc
     orc.load()
     x = make_input(0)
@@ -157,24 +297,72 @@ def run_cpu_baseline(mx_collapse):
             nbytes += nb
         reps += 1
         dt = time.perf_counter() - t0
-        if dt > 5.0 or reps >= 20:
+        if dt > 10.0 or reps >= 40:
             break
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"the full step (all ops on X[256,65536] f32) x{reps}, {dt:.2f} s single-threaded"}
 
 
+def measured_traffic(op_name):
+    """HBM bytes per launch of op_name from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    measurement (scaled by the calibration copy), or None when that op was not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(op_name)
+    except (OSError, ValueError):
+        return None
+    return rec["traffic_bytes"] if rec else None
+
+
+def kernel_probe(op_name, reps=10):
+    """For hardware-counter runs: only `op_name` of the reductions workload (reps launches on
+    rotated copies), then a 256 MiB device copy (the calibration kernel of known bytes)."""
+    import matrix_amd as mx
+    mx.init(0)
+    x = make_input(0)
+    copies = [mx.DeviceBuffer.from_numpy(x) for _ in range(N_COPIES)]
+    prepared = {p.name: p for p in (Prepared(mx, *o) for o in build_ops(mx))}
+    p = prepared[op_name]
+    if p.src != "X":
+        raise SystemExit(f"--kernel-probe: {op_name} reads an intermediate; pick an op on X")
+    for i in range(reps):
+        p.launch(mx, copies[i % N_COPIES].ptr)
+    n = 64 << 20                                     # 256 MiB of float32
+    src, dst = mx.DeviceBuffer(4 * n), mx.DeviceBuffer(4 * n)
+    src.fill_bytes(0)
+    for _ in range(reps):
+        mx.launch_copy_strided(mx.FLOAT32, mx.FLOAT32, ([n], [1], [1]), dst.ptr, src.ptr)
+    mx.sync()
+    print(json.dumps({"probe": op_name, "launches": reps, "bytes_per_launch": p.bytes,
+                      "calibration_copy_bytes": 2 * 4 * n}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
+    ap.add_argument("--kernel-probe", default=None, metavar="OP",
+                    help="run only OP of the reductions workload and a calibration copy (for counter runs)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="only the reductions workload")
     args = ap.parse_args()
+    if args.kernel_probe:
+        kernel_probe(args.kernel_probe)
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding is described in DESIGN.md, not run", file=sys.stderr)
         return 2
     r = run_gpu(args)
+    configs = {}
+    if not args.no_configs:
+        import matrix_amd as mx
+        configs["add_rowsum_f32"] = config_add_rowsum(mx)
+        configs["matmul"] = config_matmul(mx)
+        configs["conv2d"] = config_conv(mx)
+        configs["mlp_step_f32"] = config_mlp()
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(r["cpu_ops"])
     line = {
         "metric": "HBM GB/s (broadcast/reduce) + TFLOP/s (matmul/conv), % of MI355X roofline",
@@ -194,11 +382,12 @@ def main():
                                "reshape [64,4,4096,16] over axes 3 then 1",
                    "step_bytes": r["step_bytes"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(r["dominant"]),
                      "kernel": r["dominant"], "bytes_per_launch": r["dominant_bytes"],
                      "avg_ms": round(r["dominant_ms"], 5)},
         "cpu_baseline": cpu,
         "per_op_gbs": r["per_op_gbs"],
+        "configs": configs,
     }
     print(json.dumps(line), flush=True)
     return 0
