@@ -79,10 +79,11 @@ class Prepared:
         self.ws = mx.reduce_workspace_bytes(op, mx.FLOAT32, self.rs, self.n, self.desc)
         self.W = mx.DeviceBuffer(self.ws) if self.ws else None
         self.O = mx.DeviceBuffer(self.out_bytes)
+        self._launch = mx.prepare_reduce(op, mx.FLOAT32, self.rs, self.n, self.desc,
+                                         self.W.ptr if self.W else 0, self.ws)
 
     def launch(self, mx, in_ptr):
-        mx.launch_reduce(self.op, mx.FLOAT32, self.rs, self.n, self.desc, self.O.ptr, in_ptr,
-                         self.W.ptr if self.W else 0, self.ws)
+        self._launch(self.O.ptr, in_ptr)
 
 
 def run_gpu(args):
@@ -174,10 +175,13 @@ def config_add_rowsum(mx):
     desc = mx.collapse_dims3(out, b1st, b2st, out_st)
     rdesc = mx.collapse_dims_reduce2([4096, 1024], [1], [1024, 1], 1)
 
+    add = mx.prepare_bcast_binary(mx.OP_ADD, mx.FLOAT32, desc)
+    rowsum = mx.prepare_reduce(mx.RED_SUM, mx.FLOAT32, 1, 1024, rdesc)
+
     def graph(i=0):
         c = C[i % 2]
-        mx.launch_bcast_binary(mx.OP_ADD, mx.FLOAT32, desc, c.ptr, A[i % 20].ptr, B.ptr)
-        mx.launch_reduce(mx.RED_SUM, mx.FLOAT32, 1, 1024, rdesc, S.ptr, c.ptr)
+        add(c.ptr, A[i % 20].ptr, B.ptr)
+        rowsum(S.ptr, c.ptr)
 
     ms = _timed(mx, graph, 40)
     nbytes = 50_352_128
@@ -199,8 +203,8 @@ def config_matmul(mx):
         A, Bt = mx.DeviceBuffer.from_numpy(a), mx.DeviceBuffer.from_numpy(bt)
         C = mx.DeviceBuffer(16 * 2048 * 2048 * a.itemsize)
         desc = ([16, 2048, 2048], [2048 * 2048, 2048, 1], [0, 2048, 1], [2048 * 2048, 2048, 1])
-        ms = _timed(mx, lambda i=0: mx.launch_batched_matmul(code, desc, 2048, C.ptr, A.ptr, Bt.ptr),
-                    5 if dt == "f32" else 20)
+        mm = mx.prepare_batched_matmul(code, desc, 2048)
+        ms = _timed(mx, lambda i=0: mm(C.ptr, A.ptr, Bt.ptr), 5 if dt == "f32" else 20)
         tf = 274_877_906_944 / (ms * 1e-3) / 1e12
         res[f"main_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
                              "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)}
@@ -212,7 +216,8 @@ def config_matmul(mx):
         Bs = [mx.DeviceBuffer.from_numpy(bt) for _ in range(8 if dt == "f32" else 12)]
         C = mx.DeviceBuffer(8 * 4096 * a.itemsize)
         desc = ([8, 1, 4096], [4096, 4096, 1], [0, 4096, 1], [4096, 4096, 1])
-        ms = _timed(mx, lambda i=0: mx.launch_batched_matmul(code, desc, 4096, C.ptr, A.ptr, Bs[i % len(Bs)].ptr), 40)
+        mm = mx.prepare_batched_matmul(code, desc, 4096)
+        ms = _timed(mx, lambda i=0: mm(C.ptr, A.ptr, Bs[i % len(Bs)].ptr), 40)
         nbytes = (a.size + bt.size + 8 * 4096) * a.itemsize
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[f"skinny_{dt}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
@@ -257,7 +262,8 @@ def config_conv(mx):
                             k_strides=k_st, out_strides=cs([n, oh, ow, o]), pad=[pad, pad], stride=[stride, stride])
                 wsb = mx.conv_workspace_bytes(code, geom)
                 WS = mx.DeviceBuffer(max(wsb, 256))
-                ms = _timed(mx, lambda i=0: mx.launch_conv_nd(code, geom, Y.ptr, X.ptr, W.ptr, WS.ptr, wsb), 20)
+                conv = mx.prepare_conv_nd(code, geom, WS.ptr, wsb)
+                ms = _timed(mx, lambda i=0: conv(Y.ptr, X.ptr, W.ptr), 20)
                 flop = 2.0 * n * oh * ow * o * c * k * k
                 tf = flop / (ms * 1e-3) / 1e12
                 res[f"{name}_{layout}_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),

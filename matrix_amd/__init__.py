@@ -294,6 +294,50 @@ def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=
                                int(out), int(inp), int(workspace), workspace_bytes, stream))
 
 
+def prepare_bcast_binary(op, dtype, desc, stream=None):
+    """mx_launch_bcast_binary with its descriptor converted once: returns launch(R, A, B)."""
+    shape, sA, sB, sR = desc
+    fn = lib.mx_launch_bcast_binary
+    head = (op, dtype, len(shape), u32(shape), u32(sR), u32(sA), u32(sB))
+
+    def launch(R, A, B):
+        status = fn(*head, R, A, B, stream)
+        if status != OK:
+            raise MatrixAMDError(status, last_error())
+
+    return launch
+
+
+def prepare_reduce(op, dtype, reduce_stride, n_reduce, desc, workspace=0, workspace_bytes=0, stream=None):
+    """mx_launch_reduce with its descriptor converted once: returns launch(out, inp) for launches
+    repeated many times (a compiled graph node's execute)."""
+    shape, sOut, sIn = desc
+    fn = lib.mx_launch_reduce
+    head = (op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn))
+    tail = (int(workspace), workspace_bytes, stream)
+
+    def launch(out, inp):
+        status = fn(*head, out, inp, *tail)
+        if status != OK:
+            raise MatrixAMDError(status, last_error())
+
+    return launch
+
+
+def prepare_batched_matmul(dtype, desc, K, stream=None):
+    """mx_launch_batched_matmul with its descriptor converted once: returns launch(C, A, Bt)."""
+    shape, sA, sBt, sC = desc
+    fn = lib.mx_launch_batched_matmul
+    head = (dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K)
+
+    def launch(C, A, Bt):
+        status = fn(*head, C, A, Bt, stream)
+        if status != OK:
+            raise MatrixAMDError(status, last_error())
+
+    return launch
+
+
 def conv_workspace_bytes(dtype, geom):
     """geom = dict(in_shape, k_shape, out_shape, in_strides, k_strides, out_strides, groups, ...)."""
     nb = ctypes.c_size_t()
@@ -319,6 +363,24 @@ def launch_conv_nd(dtype, geom, out, inp, kern, workspace=0, workspace_bytes=0, 
                                 i32(pad), i32(stride), i32(dil), i32(dil_lhs), int(geom.get("groups", 1)),
                                 int(geom.get("flip", 0)), int(out), int(inp), int(kern), int(workspace),
                                 workspace_bytes, stream))
+
+
+def prepare_conv_nd(dtype, geom, workspace=0, workspace_bytes=0, stream=None):
+    """mx_launch_conv_nd with its geometry converted once: returns launch(out, inp, kern)."""
+    ns = len(geom["in_shape"]) - 2
+    fn = lib.mx_launch_conv_nd
+    head = (dtype, ns, u32(geom["in_shape"]), u32(geom["k_shape"]), u32(geom["out_shape"]),
+            u32(geom["in_strides"]), u32(geom["k_strides"]), u32(geom["out_strides"]),
+            i32(geom.get("pad", [0] * ns)), i32(geom.get("stride", [1] * ns)), i32(geom.get("dil", [1] * ns)),
+            i32(geom.get("dil_lhs", [1] * ns)), int(geom.get("groups", 1)), int(geom.get("flip", 0)))
+    tail = (int(workspace), workspace_bytes, stream)
+
+    def launch(out, inp, kern):
+        status = fn(*head, out, inp, kern, *tail)
+        if status != OK:
+            raise MatrixAMDError(status, last_error())
+
+    return launch
 
 
 def launch_copy_strided(dst_dtype, src_dtype, desc, dst, src, stream=None):

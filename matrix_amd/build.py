@@ -64,15 +64,30 @@ def host_sources() -> list[Path]:
     return sorted(HOST.glob("*.cpp"))
 
 
-def build_kernels(jobs: int | None = None) -> Path:
+def _stale(obj: Path, src: Path, deps: list[Path]) -> bool:
+    if not obj.exists():
+        return True
+    t = obj.stat().st_mtime
+    return any(p.stat().st_mtime > t for p in [src, *deps])
+
+
+def build_kernels(jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compiles every source (incremental=True: only objects older than their source or any
+    header of csrc/, host/ or include/) and links the library."""
     OBJ.mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     srcs = sources()
     hsrcs = host_sources()
-    cmds = [[HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(OBJ / (s.stem + ".o"))] for s in srcs]
-    cmds += [[CXX, *CXX_FLAGS, "-c", str(s), "-o", str(OBJ / ("host_" + s.stem + ".o"))] for s in hsrcs]
-    objs = [OBJ / (s.stem + ".o") for s in srcs] + [OBJ / ("host_" + s.stem + ".o") for s in hsrcs]
-    jobs = jobs or min(len(cmds), os.cpu_count() or 4, 8)
+    headers = [*CSRC.glob("*.hpp"), *HOST.glob("*.hpp"), *(ROOT / "include").glob("*.h")]
+    jobs_all = [([HIPCC, *HIP_FLAGS, "-c", str(s), "-o", str(OBJ / (s.stem + ".o"))], OBJ / (s.stem + ".o"), s)
+                for s in srcs]
+    jobs_all += [([CXX, *CXX_FLAGS, "-c", str(s), "-o", str(OBJ / ("host_" + s.stem + ".o"))],
+                  OBJ / ("host_" + s.stem + ".o"), s) for s in hsrcs]
+    cmds = [c for c, o, s in jobs_all if not incremental or _stale(o, s, headers)]
+    objs = [o for _, o, _ in jobs_all]
+    if not cmds and LIB.exists() and all(LIB.stat().st_mtime >= o.stat().st_mtime for o in objs):
+        return LIB
+    jobs = jobs or max(1, min(len(cmds), os.cpu_count() or 4, 8))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_run, c) for c in cmds]
         for f in futs:
@@ -124,8 +139,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--oracle", action="store_true", help="also build the CPU oracle")
     ap.add_argument("--programs", action="store_true", help="also build the workload and C++ test drivers")
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true", help="recompile only out-of-date objects")
     a = ap.parse_args(argv)
-    print(build_kernels(a.j))
+    print(build_kernels(a.j, incremental=a.incremental))
     if a.oracle:
         print(build_oracle())
     if a.programs:

@@ -6,7 +6,8 @@
 // K-major -- the layout MFMA wants.
 //
 // float16 / bfloat16 / float32: the matrix-core tile kernel of mfma_tile.hpp (256 x 256 tiles,
-//                     256 x 128 when N <= 128).
+//                     256 x 128 when N <= 128); at most 16 rows of A (after folding the batch):
+//                     a streaming kernel on 16 x 16 MFMAs that reads Bt once.
 // Other dtypes:       a scalar kernel accumulating in the element type (wrap-around), as the
 //                     reference's `T sum` loop does (Matrix.mm:7187-7191).
 // When Bt is shared by the whole batch (batch stride 0) and A / C stack their batches
@@ -85,6 +86,188 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(typename MmaTraits<DT>:
     C[offC + (uint64_t)m * g.ldc + (uint64_t)n * g.cn] = v;
 }
 
+// ------------------------------------------------------------------ skinny products (M <= 16)
+// A block owns 16 consecutive Bt rows (16 C columns) of one batch; its waves split the K range
+// into contiguous pieces.  Each step a lane loads one 16-byte K fragment of Bt row (n0 + l % 16)
+// and the same K fragment of A row (l % 16), at K offset 4 (l / 16) fragments, and a 16 x 16 MFMA
+// takes Bt as its row operand and A as its column operand: the result is the C^T tile, lane l
+// holding C[l % 16][n0 + 4 (l / 16) + r] in acc[r].  Rows past N or M are clamped to a valid row:
+// they only feed result rows / columns that are never stored.  Bt streams from HBM once; A (at
+// most 16 rows) is re-read from the caches.
+// The K loop is a rolling pipeline of U fragment slots: a slot is refilled with the step U ahead
+// right after its MFMA, so U steps stay in flight per wave.  Refills past the wave's last full
+// step re-read that step (a cache hit) and are discarded.  A last partial step (K not a multiple
+// of 4 fragments) is loaded with per-lane zero fill.  The waves' partial tiles are summed in wave
+// order through LDS (deterministic).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <int DT> struct SkinnyFrag;
+template <> struct SkinnyFrag<MX_FLOAT32> { using V = f4v; };
+template <> struct SkinnyFrag<MX_FLOAT16> { using V = tile::h8v; };
+template <> struct SkinnyFrag<MX_BFLOAT16> { using V = tile::b8v; };
+
+// Waves per block and steps in flight per wave, per element size (measured on the skinny
+// workload: fewer requests in flight per CU stream faster when every load instruction touches 16
+// different Bt rows): fp32 8 waves x 4 steps, 16-bit 4 waves x 4 steps.
+template <int DT> constexpr int kSkinnyWaves = DT == MX_FLOAT32 ? 8 : 4;
+constexpr int kSkinnySteps = 4;
+
+template <int DT>
+__device__ __forceinline__ f4v skinny_mma(typename SkinnyFrag<DT>::V b, typename SkinnyFrag<DT>::V a, f4v acc) {
+    if constexpr (DT == MX_FLOAT32) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(b[0], a[0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(b[1], a[1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(b[2], a[2], acc, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(b[3], a[3], acc, 0, 0, 0);
+    } else if constexpr (DT == MX_FLOAT16) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(b, a, acc, 0, 0, 0);
+    } else {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a, acc, 0, 0, 0);
+    }
+}
+
+// kw: K elements per wave (a multiple of one step, 4 fragments).  CVEC: C columns are unit-stride
+// and every 4-column group starts 4-element aligned, so a lane's 4 results go out in one store.
+template <int DT, bool CVEC>
+__global__ __launch_bounds__(64 * kSkinnyWaves<DT>) void gemm_skinny_kernel(typename MmaTraits<DT>::S* __restrict__ C,
+                                                                        const typename MmaTraits<DT>::S* __restrict__ A,
+                                                                        const typename MmaTraits<DT>::S* __restrict__ Bt,
+                                                                        GemmArgs g, uint32_t kw) {
+    using S = typename MmaTraits<DT>::S;
+    using V = typename SkinnyFrag<DT>::V;
+    constexpr uint32_t CE = 16 / sizeof(S);      // elements per fragment
+    constexpr uint32_t KS = 4 * CE;               // K per step
+    constexpr int U = kSkinnySteps;
+    constexpr int W = kSkinnyWaves<DT>;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+    const uint32_t i = lane & 15, grp = lane >> 4;
+    const uint32_t n0 = blockIdx.x * 16;
+    uint32_t b = blockIdx.y;
+    uint64_t offA = 0, offB = 0, offC = 0;
+    for (int d = g.bd.n - 1; d >= 0; --d) {
+        const uint32_t q = g.bd.shape[d].div(b);
+        const uint32_t idx = b - q * g.bd.shape[d].d;
+        b = q;
+        offA += (uint64_t)idx * g.bd.sA[d];
+        offB += (uint64_t)idx * g.bd.sB[d];
+        offC += (uint64_t)idx * g.bd.sC[d];
+    }
+    const S* brow = Bt + offB + (uint64_t)min(n0 + i, g.N - 1) * g.ldb + grp * CE;
+    const S* arow = A + offA + (uint64_t)min(i, g.M - 1) * g.lda + grp * CE;
+    const uint32_t kbeg = min(g.K, wave * kw);
+    const uint32_t kend = min(g.K, kbeg + kw);
+    const uint32_t nfull = (kend - kbeg) / KS;              // full steps of this wave
+    f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+    if (nfull > 0) {
+        const S* bw = brow + kbeg;
+        const S* aw = arow + kbeg;
+        const uint32_t last = (nfull - 1) * KS;
+        V fb[U], fa[U];
+        // slot order in the prologue as in the loop, so on entry slot u is the u-th oldest load
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t o = min((uint32_t)u * KS, last);
+            fb[u] = *reinterpret_cast<const V*>(bw + o);
+            fa[u] = *reinterpret_cast<const V*>(aw + o);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // whole rounds of U steps: no branch inside, so each MFMA waits only for its own slot
+        const uint32_t rounds = nfull / U;
+        for (uint32_t r = 0; r < rounds; r++) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (u & 1) acc1 = skinny_mma<DT>(fb[u], fa[u], acc1);
+                else acc0 = skinny_mma<DT>(fb[u], fa[u], acc0);
+                const uint32_t o = min(((r + 1) * U + u) * KS, last);
+                fb[u] = *reinterpret_cast<const V*>(bw + o);
+                fa[u] = *reinterpret_cast<const V*>(aw + o);
+            }
+            // keep the order slot by slot: its MFMAs (mask 0x008), then its two refills (0x020),
+            // so the refill of slot u is in flight while slots u + 1 .. are consumed
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, DT == MX_FLOAT32 ? 4 : 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+            }
+        }
+        // the remaining nfull % U steps were loaded by the last round's refills
+        const uint32_t rem = nfull % U;
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if ((uint32_t)u < rem) acc0 = skinny_mma<DT>(fb[u], fa[u], acc0);
+    }
+    const uint32_t kt = kbeg + nfull * KS;                 // partial last step, if any
+    if (kt < kend) {
+        const bool ok = kt + grp * CE < kend;
+        const V zero = {};
+        const V bv = ok ? *reinterpret_cast<const V*>(brow + kt) : zero;
+        const V av = ok ? *reinterpret_cast<const V*>(arow + kt) : zero;
+        acc0 = skinny_mma<DT>(bv, av, acc0);
+    }
+    f4v acc = acc0 + acc1;
+    __shared__ f4v part[W - 1][64];
+    if (wave > 0) part[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < W - 1; w++) acc += part[w][lane];
+    if (i >= g.M) return;
+    const uint32_t nb = n0 + 4 * grp;
+    S* crow = C + offC + (uint64_t)i * g.ldc;
+    S o[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if constexpr (DT == MX_FLOAT32) o[r] = acc[r];
+        else if constexpr (DT == MX_FLOAT16) o[r] = float_to_half_bits(acc[r]);
+        else o[r] = float_to_bf16(acc[r]);
+    }
+    if constexpr (CVEC) {
+        if (nb < g.N) {              // N % 4 == 0 on this path: the whole group is in range
+            struct alignas(4 * sizeof(S)) Q { S v[4]; } q{{o[0], o[1], o[2], o[3]}};
+            *reinterpret_cast<Q*>(crow + nb) = q;
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (nb + r < g.N) crow[(uint64_t)(nb + r) * g.cn] = o[r];
+    }
+}
+
+// The skinny path applies to 16-bit and fp32 data with unit K strides, 16-byte aligned rows and
+// K a whole number of fragments, at most 16 rows of A, and enough column tiles to fill the CUs.
+template <int DT>
+bool skinny_ok(const GemmArgs& g, const void* A, const void* Bt) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr uint32_t CE = 16 / sizeof(S);
+    if (g.M > 16 || g.ka != 1 || g.kb != 1 || g.K % CE || g.lda % CE || g.ldb % CE) return false;
+    if ((uintptr_t)A % 16 || (uintptr_t)Bt % 16 || g.batches > 65535) return false;
+    for (int d = 0; d < g.bd.n; d++)
+        if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
+    return (uint64_t)((g.N + 15) / 16) * g.batches >= 128;
+}
+
+template <int DT>
+int launch_skinny(const GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr uint32_t KS = 4 * (16 / sizeof(S));
+    constexpr int W = kSkinnyWaves<DT>;
+    uint32_t kw = (g.K + W - 1) / W;
+    kw = (kw + KS - 1) / KS * KS;
+    bool cvec = g.cn == 1 && g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)C % (4 * sizeof(S)) == 0;
+    for (int d = 0; cvec && d < g.bd.n; d++)
+        if (g.bd.sC[d] % 4) cvec = false;
+    const dim3 grid((g.N + 15) / 16, g.batches);
+    if (cvec)
+        hipLaunchKernelGGL((gemm_skinny_kernel<DT, true>), grid, dim3(64 * W), 0, st, (S*)C, (const S*)A,
+                           (const S*)Bt, g, kw);
+    else
+        hipLaunchKernelGGL((gemm_skinny_kernel<DT, false>), grid, dim3(64 * W), 0, st, (S*)C, (const S*)A,
+                           (const S*)Bt, g, kw);
+    MX_HIP(hipGetLastError());
+    return MX_OK;
+}
+
 // Split-K when the output tiles leave most of the 256 CUs idle: enough K pieces (each at least
 // four 128-byte K pairs) to give about two blocks per CU.  Returns 1 for no split.
 uint32_t choose_split(const tile::TileShape& ts, const GemmArgs& g, uint32_t pair_elems, uint32_t* ksplit) {
@@ -103,6 +286,7 @@ template <int DT>
 int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
     using S = typename MmaTraits<DT>::S;
     constexpr int CE = 16 / sizeof(S);
+    if (skinny_ok<DT>(g, A, Bt)) return launch_skinny<DT>(g, C, A, Bt, st);
     const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
     uint32_t ksplit = 0;
     const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);

@@ -14,11 +14,17 @@
 // (deterministic run to run, within tolerance of the sequential sum).
 //
 // Plans, chosen on the host from the CollapsedDims_2 descriptor:
-//   rows   reduce stride 1, short or medium rows: L lanes per output (L = 1, 4, 16, 64),
-//          128-bit loads, several outputs in flight per lane group;
-//   block  reduce stride 1, long rows: one 256-thread block per (output, 32 KB chunk);
-//   cols   reduce stride != 1: a lane owns VEC consecutive outputs, the waves of a block
-//          split the reduced axis between them and combine through LDS.
+//   lane   reduce stride 1, rows of at most four 128-bit vectors: one lane per output, every
+//          load of the row issued before the first compare;
+//   rows   reduce stride 1, medium rows: L lanes per output (L = 4, 16, 64), 128-bit loads,
+//          several outputs in flight per lane group;
+//   block  reduce stride 1, long rows: a 1024- or 256-thread block per output (or per chunk);
+//   short  reduce stride != 1, at most 8 reduced elements: a lane owns VEC consecutive outputs
+//          and issues all of their loads at once;
+//   cols   reduce stride != 1, longer axes: a lane owns VEC consecutive outputs, the four waves
+//          of a block split the reduced axis between them and combine through LDS.
+// Loads in flight per lane are kept moderate (4-8 vectors): on this part a 64 MiB read is
+// fastest with about 1-4 KiB in flight per wave; more queued requests per CU slow it down.
 // The plans avoid splitting one output's axis over blocks whenever the outputs alone cover the
 // CUs; when they must split, each block writes its partial to the workspace and a second launch
 // combines the partials in split order.
@@ -202,9 +208,36 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(
     }
 }
 
+// ------------------------------------------------------------------ lane (stride 1, rows of <= 4 vectors)
+// One lane per output; the nv <= NV vectors of the row are all loaded before any is used.
+template <int DT, int OP, int VEC, int NV>
+__global__ __launch_bounds__(256) void reduce_lane_kernel(
+    typename RedSel<DT, OP>::R::OutT* __restrict__ out, const typename dt_traits<DT>::S* __restrict__ in,
+    uint32_t total_out, uint32_t nv, OffDesc od) {
+    using R = typename RedSel<DT, OP>::R;
+    using S = typename dt_traits<DT>::S;
+    using V = VecT<S, VEC>;
+    const uint32_t g = blockIdx.x * 256 + threadIdx.x;
+    if (g >= total_out) return;
+    const S* row = in + od.offset(g);
+    V v[NV];
+#pragma unroll
+    for (int u = 0; u < NV; u++)
+        if (u < nv) v[u] = *reinterpret_cast<const V*>(row + u * VEC);
+    typename R::St st = R::init();
+#pragma unroll
+    for (int u = 0; u < NV; u++)
+        if (u < nv) {
+#pragma unroll
+            for (int k = 0; k < VEC; k++) R::step(st, v[u].v[k], u * VEC + k);
+        }
+    out[g] = R::out(st);
+}
+
 // ------------------------------------------------------------------ block (stride 1, long rows)
 // One block of 64 * WAVES threads per (output, chunk).  blockIdx.x = output, blockIdx.y = chunk.
-template <int DT, int OP, int VEC, int WAVES>
+// U vectors per lane are in flight; the last partial round issues its loads together.
+template <int DT, int OP, int VEC, int WAVES, int U>
 __global__ __launch_bounds__(64 * WAVES) void reduce_block_kernel(
     typename RedSel<DT, OP>::R::OutT* __restrict__ out, typename RedSel<DT, OP>::R::St* __restrict__ part,
     const typename dt_traits<DT>::S* __restrict__ in, uint32_t total_out,
@@ -213,7 +246,6 @@ __global__ __launch_bounds__(64 * WAVES) void reduce_block_kernel(
     using S = typename dt_traits<DT>::S;
     using V = VecT<S, VEC>;
     using St = typename R::St;
-    constexpr int U = 8;
     constexpr uint32_t STEP = 64 * WAVES * VEC;
     const uint32_t g = blockIdx.x;
     const uint32_t c = blockIdx.y;
@@ -231,10 +263,17 @@ __global__ __launch_bounds__(64 * WAVES) void reduce_block_kernel(
 #pragma unroll
             for (int k = 0; k < VEC; k++) R::step(st, v[u].v[k], e + u * STEP + k);
     }
-    for (; e < end; e += STEP) {
-        V v = *reinterpret_cast<const V*>(row + e);
+    if constexpr (U > 1) if (e < end) {
+        V v[U - 1];
 #pragma unroll
-        for (int k = 0; k < VEC; k++) R::step(st, v.v[k], e + k);
+        for (int u = 0; u < U - 1; u++)
+            if (e + u * STEP < end) v[u] = *reinterpret_cast<const V*>(row + e + u * STEP);
+#pragma unroll
+        for (int u = 0; u < U - 1; u++)
+            if (e + u * STEP < end) {
+#pragma unroll
+                for (int k = 0; k < VEC; k++) R::step(st, v[u].v[k], e + u * STEP + k);
+            }
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) st = R::combine(st, R::shfl(st, m));
@@ -285,10 +324,17 @@ __global__ __launch_bounds__(64 * WAVES) void reduce_cols_kernel(
 #pragma unroll
                 for (int k = 0; k < VEC; k++) R::step(st[k], v[u].v[k], i + u * WAVES);
         }
-        for (; i < end; i += WAVES) {
-            V v = *reinterpret_cast<const V*>(base + (uint64_t)i * rs);
+        if (i < end) {
+            V v[U - 1];
 #pragma unroll
-            for (int k = 0; k < VEC; k++) R::step(st[k], v.v[k], i);
+            for (int u = 0; u < U - 1; u++)
+                if (i + u * WAVES < end) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)(i + u * WAVES) * rs);
+#pragma unroll
+            for (int u = 0; u < U - 1; u++)
+                if (i + u * WAVES < end) {
+#pragma unroll
+                    for (int k = 0; k < VEC; k++) R::step(st[k], v[u].v[k], i + u * WAVES);
+                }
         }
     }
     // combine the waves' states through LDS, in wave order
@@ -311,6 +357,45 @@ __global__ __launch_bounds__(64 * WAVES) void reduce_cols_kernel(
             if (nsplit == 1) out[g0 + k] = R::out(st[k]);
             else part[(uint64_t)c * total_out + g0 + k] = st[k];
         }
+    }
+}
+
+// ------------------------------------------------------------------ short (stride != 1, n <= 8)
+// Lane l of wave w owns outputs [((blockIdx.x * WAVES + w) * 64 + l) * VEC, +VEC) and loads all
+// n <= NMAX of their rows at once.  VST: the output is 16-byte aligned and VEC outputs make 16
+// bytes, so they go out in one store.
+template <int DT, int OP, int VEC, int NMAX, int WAVES, bool VST>
+__global__ __launch_bounds__(64 * WAVES) void reduce_short_kernel(
+    typename RedSel<DT, OP>::R::OutT* __restrict__ out, const typename dt_traits<DT>::S* __restrict__ in,
+    uint32_t total_out, uint32_t n, uint32_t rs, OffDesc od) {
+    using R = typename RedSel<DT, OP>::R;
+    using S = typename dt_traits<DT>::S;
+    using V = VecT<S, VEC>;
+    using OutT = typename R::OutT;
+    const uint32_t g0 = ((blockIdx.x * WAVES + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63)) * VEC;
+    if (g0 >= total_out) return;
+    const S* base = in + od.offset(g0);
+    V v[NMAX];
+#pragma unroll
+    for (int u = 0; u < NMAX; u++)
+        if (u < n) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)u * rs);
+    typename R::St st[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; k++) st[k] = R::init();
+#pragma unroll
+    for (int u = 0; u < NMAX; u++)
+        if (u < n) {
+#pragma unroll
+            for (int k = 0; k < VEC; k++) R::step(st[k], v[u].v[k], u);
+        }
+    if constexpr (VST) {
+        VecT<OutT, VEC> o;
+#pragma unroll
+        for (int k = 0; k < VEC; k++) o.v[k] = R::out(st[k]);
+        *reinterpret_cast<VecT<OutT, VEC>*>(out + g0) = o;
+    } else {
+#pragma unroll
+        for (int k = 0; k < VEC; k++) out[g0 + k] = R::out(st[k]);
     }
 }
 
@@ -346,7 +431,7 @@ __global__ __launch_bounds__(256) void reduce_finalize_wide_kernel(
 }
 
 // ------------------------------------------------------------------ planning
-enum Mode { kRows = 0, kBlockMode = 1, kCols = 2 };
+enum Mode { kRows = 0, kBlockMode = 1, kCols = 2, kLane = 3, kShort = 4 };
 
 struct Desc {
     int cd;
@@ -359,7 +444,8 @@ struct Plan {
     int vec = 1;            // elements per 128-bit load actually used (1 = scalar loads)
     int lanes = 1;          // rows plan: lanes per output
     int unroll = 1;         // rows plan: outputs in flight per lane group
-    int waves = 1;          // cols plan: waves per block
+    int waves = 1;          // cols / block / short plans: waves per block
+    uint32_t nv = 0;        // lane plan: vectors per row
     uint32_t blocks = 0;    // rows plan: grid size; cols plan: column groups
     uint32_t rounds = 0;
     uint32_t nsplit = 1;    // blocks sharing one output's axis
@@ -370,7 +456,6 @@ struct Plan {
 };
 
 constexpr uint32_t kTargetBlocks = 2048;     // 8 resident 256-thread blocks per CU on 256 CUs
-constexpr uint64_t kColsLdsBytes = 32768;    // LDS budget of the cols plan's cross-wave combine
 
 // The split layout depends only on the descriptor (never on pointer alignment), so the
 // workspace size reported ahead of time always covers the launch.
@@ -389,7 +474,14 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
         const uint32_t nominal = v_ok ? (uint32_t)VEC : 1u;
         p.vec = (v_ok && aligned) ? VEC : 1;
         const uint32_t nv = (d.n + nominal - 1) / nominal;
-        if (nv > 1024) {
+        if (nv <= 4) {
+            p.mode = kLane;
+            p.nv = p.vec == VEC ? nv : d.n;     // unaligned input: scalar loads (n <= 4 * VEC)
+            if (p.nv > 4) p.mode = kRows;       // unaligned and n > 4: the rows plan below
+        }
+        if (p.mode == kLane) {
+            p.blocks = (uint32_t)((tot + 255) / 256);
+        } else if (nv > 1024) {
             // One block per output when there are enough outputs to cover the CUs (no partials,
             // no cross-block step); otherwise split each row into chunks of >= 4 vectors a thread.
             p.mode = kBlockMode;
@@ -423,17 +515,23 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
                 d.rs % VEC == 0;
     for (int i = 0; v_ok && i < last; i++) if (d.si[i] % VEC || d.so[i] % VEC) v_ok = false;
     const uint32_t nominal = v_ok ? (uint32_t)VEC : 1u;
-    p.mode = kCols;
     p.vec = (v_ok && aligned) ? VEC : 1;
-    p.waves = d.n >= 64 ? 16 : (d.n >= 16 ? 4 : 1);
-    if (p.waves == 16 && 15ull * 64 * nominal * stbytes > kColsLdsBytes) p.waves = 4;
-    const uint64_t groups = (tot + 64ull * nominal - 1) / (64ull * nominal);   // blocks along x
+    const uint64_t groups = (tot + 64ull * nominal - 1) / (64ull * nominal);   // 64-lane column groups
     p.blocks = (uint32_t)groups;
-    // split the axis over blocks when the grid would leave CUs idle
-    const uint64_t waves_total = groups * p.waves;
+    if (d.n <= 8) {
+        // every row load of a lane in flight at once; one wave per block while the groups alone
+        // give every CU several waves, else four
+        p.mode = kShort;
+        p.waves = groups >= 4096 ? 1 : 4;
+        p.chunk = d.n;
+        return p;
+    }
+    p.mode = kCols;
+    p.waves = 4;
+    // split the axis over blocks when there are fewer column groups than CUs
     p.nsplit = 1;
-    if (waves_total < 4096 && d.n >= 256) {
-        uint64_t want = (4096 + waves_total - 1) / waves_total;
+    if (groups < 256 && d.n >= 256) {
+        uint64_t want = (512 + groups - 1) / groups;
         uint64_t maxc = d.n / 128;                 // keep >= 128 axis elements per split
         if (maxc > 4096) maxc = 4096;
         uint64_t nc = want < maxc ? want : maxc;
@@ -468,7 +566,28 @@ int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, h
     const S* in = (const S*)inp;
     StT* part = (StT*)ws;
     const bool vec = p.vec == VEC && VEC > 1;
-    if (p.mode == kRows) {
+    if (p.mode == kLane) {
+        dim3 grid(p.blocks);
+        if (vec) hipLaunchKernelGGL((reduce_lane_kernel<DT, OP, VEC, 4>), grid, dim3(256), 0, st, out, in, p.total_out, p.nv, od);
+        else hipLaunchKernelGGL((reduce_lane_kernel<DT, OP, 1, 4>), grid, dim3(256), 0, st, out, in, p.total_out, p.nv, od);
+    } else if (p.mode == kShort) {
+        const uint32_t gx = (uint32_t)((p.total_out + 64ull * p.waves * p.vec - 1) / (64ull * p.waves * p.vec));
+#define MX_SHORT(V_, W_, VST_) hipLaunchKernelGGL((reduce_short_kernel<DT, OP, V_, 8, W_, VST_>), dim3(gx), dim3(64 * W_), 0, st, \
+                                                  out, in, p.total_out, d.n, d.rs, od)
+        constexpr bool kVst = sizeof(OutT) * VEC == 16;   // VEC outputs fill one 128-bit store
+        bool done = false;
+        if constexpr (kVst) {
+            if (vec && (uintptr_t)outp % 16 == 0) {
+                if (p.waves == 1) MX_SHORT(VEC, 1, true); else MX_SHORT(VEC, 4, true);
+                done = true;
+            }
+        }
+        if (!done) {
+            if (vec) { if (p.waves == 1) MX_SHORT(VEC, 1, false); else MX_SHORT(VEC, 4, false); }
+            else { if (p.waves == 1) MX_SHORT(1, 1, false); else MX_SHORT(1, 4, false); }
+        }
+#undef MX_SHORT
+    } else if (p.mode == kRows) {
         dim3 grid(p.blocks);
 #define MX_ROWS(V_, L_, U_) hipLaunchKernelGGL((reduce_rows_kernel<DT, OP, V_, L_, U_>), grid, dim3(256), 0, st, \
                                                out, in, p.total_out, d.n, p.rounds, od)
@@ -482,12 +601,12 @@ int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, h
 #undef MX_ROWS
     } else if (p.mode == kBlockMode) {
         dim3 grid(p.total_out, p.nsplit);
-#define MX_BLOCK(V_, W_) hipLaunchKernelGGL((reduce_block_kernel<DT, OP, V_, W_>), grid, dim3(64 * W_), 0, st, \
-                                            out, part, in, p.total_out, d.n, p.chunk, p.nsplit, od)
+#define MX_BLOCK(V_, W_, U_) hipLaunchKernelGGL((reduce_block_kernel<DT, OP, V_, W_, U_>), grid, dim3(64 * W_), 0, st, \
+                                                out, part, in, p.total_out, d.n, p.chunk, p.nsplit, od)
         if (vec) {
-            if (p.waves == 16) MX_BLOCK(VEC, 16); else MX_BLOCK(VEC, 4);
+            if (p.waves == 16) MX_BLOCK(VEC, 16, 4); else MX_BLOCK(VEC, 4, 8);
         } else {
-            if (p.waves == 16) MX_BLOCK(1, 16); else MX_BLOCK(1, 4);
+            if (p.waves == 16) MX_BLOCK(1, 16, 4); else MX_BLOCK(1, 4, 8);
         }
 #undef MX_BLOCK
     } else {
@@ -496,15 +615,8 @@ int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, h
         dim3 grid(gx, p.nsplit);
 #define MX_COLS(V_, W_) hipLaunchKernelGGL((reduce_cols_kernel<DT, OP, V_, W_>), grid, dim3(64 * W_), 0, st, \
                                            out, part, in, p.total_out, d.n, d.rs, p.chunk, p.nsplit, od)
-        if (vec) {
-            if constexpr (15ull * 64 * VEC * sizeof(StT) <= kColsLdsBytes) {
-                switch (p.waves) { case 16: MX_COLS(VEC, 16); break; case 4: MX_COLS(VEC, 4); break; default: MX_COLS(VEC, 1); break; }
-            } else {
-                switch (p.waves) { case 4: MX_COLS(VEC, 4); break; default: MX_COLS(VEC, 1); break; }
-            }
-        } else {
-            switch (p.waves) { case 16: MX_COLS(1, 16); break; case 4: MX_COLS(1, 4); break; default: MX_COLS(1, 1); break; }
-        }
+        if (vec) MX_COLS(VEC, 4);
+        else MX_COLS(1, 4);
 #undef MX_COLS
     }
     MX_HIP(hipGetLastError());

@@ -174,3 +174,39 @@ def test_integer_matmul_exact(mx, orc, dt):
         bt = rng.integers(info.min, info.max, [2, 5, 9], dtype=npt, endpoint=True)
     got, ref, _ = run_mm(mx, orc, code, a, bt)
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
+    ([8, 1, 4096], [4096, 4096]),        # the skinny workload (batch folds into M = 8)
+    ([16, 3000], [2050, 3000]),          # M = 16, ragged N (scalar stores), K not a step multiple
+    ([1, 1024], [2048, 1024]),           # one row
+    ([3, 5, 520], [3, 2048, 520]),       # per-batch Bt: blockIdx.y walks the batch
+    ([2, 2, 7, 64], [2, 1, 1024, 64]),   # two batch axes, one broadcast; K shorter than the waves' split
+    ([4, 40], [4096, 40]),               # K = 40: most waves idle, K tail inside a step
+])
+def test_skinny_path(mx, orc, dt, case):
+    """At most 16 rows of A after folding: the 16 x 16 MFMA streaming kernel."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(14)
+    a_shape, bt_shape = case
+    K = a_shape[-1]
+    a = gen(rng, code, a_shape, 1.0 / math.sqrt(K), mx)
+    bt = gen(rng, code, bt_shape, 1.0, mx)
+    got, ref, _ = run_mm(mx, orc, code, a, bt)
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
+    if code == mx.FLOAT32:
+        ref64 = np.matmul(a.astype(np.float64), np.swapaxes(bt.astype(np.float64), -1, -2))
+        assert normwise_rel(got, ref64.reshape(-1)) <= 1e-5
+
+
+def test_skinny_one_hot_exact(mx, orc):
+    """One-hot A rows pick Bt columns exactly: C[m, n] = Bt[n, k_m]."""
+    rng = np.random.default_rng(15)
+    K, N = 512, 4096
+    ks = rng.integers(0, K, 16)
+    a = np.zeros([16, K], np.float32)
+    a[np.arange(16), ks] = 1.0
+    bt = rng.standard_normal([N, K]).astype(np.float32)
+    got, _, _ = run_mm(mx, orc, mx.FLOAT32, a, bt)
+    assert np.array_equal(got.reshape(16, N), bt[:, ks].T)

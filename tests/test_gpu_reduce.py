@@ -40,8 +40,7 @@ def run_reduce(mx, orc, op, code, x_flat, shape, axis, in_strides=None, keepdims
     mx.sync()
     got = O.download(out_dt, total)
     if W:
-        # the split plan leaves its arrival counters at zero: a second launch on the same
-        # workspace gives the same bits
+        # split plans: a second launch on the same workspace gives the same bits
         O2 = mx.DeviceBuffer(max(total, 1) * np.dtype(out_dt).itemsize)
         mx.launch_reduce(op, code, rs, n, desc, O2.ptr, X.ptr, W.ptr, wsb)
         mx.sync()
@@ -255,3 +254,61 @@ def test_split_rows_few_outputs(mx, orc, opn):
         check_sum(got, ref, np.abs(x.astype(np.float64)).sum(1))
     else:
         assert np.array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize("dt,shape,axis", [
+    ("FLOAT32", [5000, 16], 1), ("FLOAT32", [333, 8], 1), ("FLOAT32", [777, 12], 1), ("FLOAT32", [100, 4], 1),
+    ("FLOAT16", [900, 32], 1), ("BFLOAT16", [257, 24], 1), ("INT8", [300, 64], 1), ("INT64", [500, 6], 1),
+    ("FLOAT32", [2, 300000], 0), ("FLOAT32", [7, 40000], 0), ("FLOAT32", [8, 36], 0), ("FLOAT32", [3, 5, 64], 1),
+    ("FLOAT16", [5, 4096], 0), ("INT8", [6, 4096], 0), ("UINT16", [4, 1000], 0), ("INT64", [8, 130], 0),
+    ("FLOAT32", [13, 4096], 0), ("FLOAT32", [24, 520], 0), ("FLOAT16", [31, 96], 0), ("FLOAT32", [9, 3, 40], 0)])
+@pytest.mark.parametrize("opn", OPS)
+def test_plans_lane_short_and_tails(mx, orc, dt, shape, axis, opn):
+    """Rows of <= 4 vectors (one lane per output), strided axes of <= 8 elements (all loads at
+    once, 1 or 4 waves per block, 128-bit output stores) and strided axes of 9..31 elements
+    (only the predicated tail of the four-wave columns plan runs)."""
+    code, op = getattr(mx, dt), getattr(mx, opn)
+    npt = mx.NP_DTYPE[code]
+    rng = np.random.default_rng(7)
+    xf = np.round(rng.standard_normal(shape) * 3)
+    if code == mx.FLOAT32:
+        x = xf.astype(np.float32)
+        x[rng.random(shape) < 0.1] *= -0.0
+    elif code == mx.FLOAT16:
+        x = xf.astype(np.float16)
+    elif code == mx.BFLOAT16:
+        from oracle.oracle import f32_to_bf16_bits
+        x = f32_to_bf16_bits(xf.astype(np.float32))
+    else:
+        info = np.iinfo(npt)
+        x = rng.integers(info.min, info.max, size=shape, dtype=npt, endpoint=True)
+    got, ref, *_ = run_reduce(mx, orc, op, code, x.ravel(), shape, axis)
+    if op == mx.RED_SUM and code == mx.FLOAT32:
+        check_sum(got, ref, abs_sum(mx, x.ravel(), shape, axis))
+    else:
+        # integer-valued 16-bit floats sum exactly in fp32, so both round the same exact sum
+        assert np.array_equal(bits(got), bits(ref)), (dt, shape, axis, opn)
+
+
+@pytest.mark.parametrize("opn", OPS)
+def test_unaligned_input_and_output(mx, orc, opn):
+    """Views at a 4-byte offset: scalar loads for the lane / short plans, scalar output stores."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(8)
+    for shape, axis in [([600, 16], 1), ([600, 4], 1), ([6, 8192], 0), ([4, 4, 512], 1)]:
+        x = np.round(rng.standard_normal(shape) * 3).astype(np.float32)
+        desc, rs, n, total = reduce_desc(mx, shape, axis)
+        X = mx.DeviceBuffer(x.nbytes + 16)
+        X.upload(np.concatenate([np.zeros(1, np.float32), x.ravel()]).view(np.uint8))
+        out_dt = np.int32 if op in (mx.RED_ARGMAX, mx.RED_ARGMIN) else np.float32
+        O = mx.DeviceBuffer(total * 4 + 16)
+        wsb = mx.reduce_workspace_bytes(op, mx.FLOAT32, rs, n, desc)
+        W = mx.DeviceBuffer(wsb) if wsb else None
+        mx.launch_reduce(op, mx.FLOAT32, rs, n, desc, O.ptr + 4, X.ptr + 4, W.ptr if W else 0, wsb)
+        mx.sync()
+        got = O.download(out_dt, total + 1)[1:]
+        ref = orc.reduce(op, mx.FLOAT32, rs, n, desc, total, x.ravel(), acc=orc.ACC_F32)
+        if op == mx.RED_SUM:
+            check_sum(got, ref, abs_sum(mx, x.ravel(), shape, axis))
+        else:
+            assert np.array_equal(bits(got), bits(ref)), (shape, axis)
