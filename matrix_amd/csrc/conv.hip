@@ -192,6 +192,43 @@ __global__ __launch_bounds__(256) void pack_input_transpose_kernel(S* __restrict
     }
 }
 
+// The same transpose with 16-byte accesses on both sides (positions per image, channel stride,
+// image stride and the source all in whole 16-byte units).  Lane (cb = l % 8, pb = l / 8) of wave
+// w loads VE channel rows (VE = elements per 16 bytes) of VE consecutive positions, transposes the
+// VE x VE block in registers and stores VE position rows of VE channels: per instruction, 8 lanes
+// cover 128 contiguous bytes of one channel row (loads) or of one position row (stores).
+// Channels in [C, Cgp) are written as zeros.
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input_transpose16_kernel(S* __restrict__ xp, const S* __restrict__ in,
+                                                                     uint32_t P, uint32_t C, uint32_t Cgp, uint64_t sN,
+                                                                     uint64_t sC) {
+    constexpr int VE = 16 / sizeof(S);
+    struct alignas(16) V { S v[VE]; };
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t c = blockIdx.y * (8 * VE) + (lane & 7) * VE;
+    const uint32_t p = (blockIdx.x * 32 + wave * 8 + (lane >> 3)) * VE;
+    if (p >= P || c >= Cgp) return;
+    const S* src = in + (uint64_t)blockIdx.z * sN + p;
+    // rows past C load a valid row (no branch between the loads) and are zeroed afterwards
+    V v[VE];
+#pragma unroll
+    for (int i = 0; i < VE; i++) v[i] = *reinterpret_cast<const V*>(src + (uint64_t)min(c + i, C - 1) * sC);
+#pragma unroll
+    for (int i = 0; i < VE; i++)
+        if (c + i >= C) {
+#pragma unroll
+            for (int j = 0; j < VE; j++) v[i].v[j] = S(0);
+        }
+    S* dst = xp + ((uint64_t)blockIdx.z * P + p) * Cgp + c;
+#pragma unroll
+    for (int j = 0; j < VE; j++) {
+        V w;
+#pragma unroll
+        for (int i = 0; i < VE; i++) w.v[i] = v[i].v[j];
+        *reinterpret_cast<V*>(dst + (uint64_t)j * Cgp) = w;
+    }
+}
+
 // Wp[o, k.., c] = c < Cg ? kern[o, (flip ? K - 1 - k : k).., c] : 0.
 struct PackKDesc {
     int ns;
@@ -202,21 +239,24 @@ struct PackKDesc {
     uint64_t s[kMaxSpatial + 2];
 };
 
+// The launcher keeps total below 2^32, so the index decomposes with 32-bit FastDiv.
 template <typename S>
 __global__ __launch_bounds__(256) void pack_kernel_kernel(S* __restrict__ wp, const S* __restrict__ kern,
-                                                          uint64_t total, PackKDesc d) {
-    const uint64_t stride = (uint64_t)gridDim.x * 256;
-    for (uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
-        uint64_t rem = t;
-        const uint32_t c = (uint32_t)(rem % d.dims[d.ns + 1].d);
-        rem /= d.dims[d.ns + 1].d;
+                                                          uint32_t total, PackKDesc d) {
+    const uint32_t stride = gridDim.x * 256;
+    for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+        uint32_t rem = t;
+        uint32_t q = d.dims[d.ns + 1].div(rem);
+        const uint32_t c = rem - q * d.dims[d.ns + 1].d;
+        rem = q;
         uint64_t off = (uint64_t)c * d.s[d.ns + 1];
         for (int a = d.ns; a >= 1; --a) {
-            const uint32_t k = (uint32_t)(rem % d.dims[a].d);
-            rem /= d.dims[a].d;
+            q = d.dims[a].div(rem);
+            const uint32_t k = rem - q * d.dims[a].d;
+            rem = q;
             off += (uint64_t)(d.flip ? d.K[a - 1] - 1 - k : k) * d.s[a];
         }
-        off += rem * d.s[0];
+        off += (uint64_t)rem * d.s[0];
         wp[t] = c < d.Cg ? kern[off] : S(0);
     }
 }
@@ -380,6 +420,15 @@ int launch_pack_input(const ConvShape& cs, uint32_t Cgp, S* xp, const S* in, hip
     for (int d = cs.ns - 1; d >= 1 && run; --d) run = cs.in_s[d] == cs.in_s[d + 1] * cs.S[d];
     uint64_t P = 1;
     for (int d = 0; d < cs.ns; d++) P *= cs.S[d];
+    constexpr uint32_t VE = 16 / sizeof(S);
+    if (run && P < (1ull << 31) && cs.N < 65536 && P % VE == 0 && cs.in_s[cs.ns + 1] % VE == 0 &&
+        cs.in_s[0] % VE == 0 && Cgp % VE == 0 && (uintptr_t)in % 16 == 0 && (uintptr_t)xp % 16 == 0) {
+        dim3 grid((uint32_t)((P + 32 * VE - 1) / (32 * VE)), (Cgp + 8 * VE - 1) / (8 * VE), cs.N);
+        hipLaunchKernelGGL((pack_input_transpose16_kernel<S>), grid, dim3(256), 0, st, xp, in, (uint32_t)P, cs.C, Cgp,
+                           cs.in_s[0], cs.in_s[cs.ns + 1]);
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    }
     if (run && P < (1ull << 31) && cs.N < 65536) {
         dim3 grid((uint32_t)((P + 63) / 64), (Cgp + 63) / 64, cs.N);
         hipLaunchKernelGGL((pack_input_transpose_kernel<S>), grid, dim3(256), 0, st, xp, in, (uint32_t)P, cs.C, Cgp,
@@ -418,9 +467,10 @@ int launch_pack_kernel(const ConvShape& cs, uint32_t Cgp, int flip, S* wp, const
     d.Cg = cs.Cg;
     d.flip = flip;
     for (int a = 0; a < cs.ns + 2; a++) d.s[a] = cs.k_s[a];
+    if (total > 0xffffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: kernel of 2^32 or more elements");
     const uint64_t want = (total + 255) / 256;
     hipLaunchKernelGGL((pack_kernel_kernel<S>), dim3((uint32_t)(want < 65536 ? want : 65536)), dim3(256), 0, st, wp,
-                       kern, total, d);
+                       kern, (uint32_t)total, d);
     MX_HIP(hipGetLastError());
     return MX_OK;
 }

@@ -94,6 +94,8 @@ def oihw_view(o, i, kh, kw):
     (1, 3, 10, 10, 16, 3, 3, 1, 1, "nhwc"),        # 3 channels: zero-padded K pair
     (3, 64, 6, 6, 160, 3, 3, 1, 1, "nhwc"),        # O > 128: 256-wide N tiles
     (1, 96, 5, 5, 8, 5, 5, 2, 1, "nchw"),          # kernel as large as the image
+    (2, 64, 28, 28, 32, 3, 3, 1, 1, "nchw"),       # NCHW pack with 16-byte register transposes
+    (2, 20, 8, 8, 16, 3, 3, 1, 1, "nchw"),         # the same with zero channels C..Cgp
 ])
 def test_conv2d_mfma(mx, orc, dt, case):
     code = getattr(mx, dt)
