@@ -13,8 +13,9 @@
 //   - anything -> bool is (value != 0); bool reads as 0 / 1.
 //
 // Layout: the iteration space is a collapsed descriptor (any cdims <= 8).  Same-dtype copies
-// whose innermost axis is unit-stride on both sides move 16 bytes per thread; everything else
-// runs one element per thread with FastDiv index decomposition.
+// whose innermost axis is unit-stride on both sides move 16 bytes per thread; same-dtype
+// transposes (16-byte aligned) move 16-byte register blocks; everything else runs one element
+// per thread with FastDiv index decomposition.
 #include "common.hpp"
 
 namespace mx {
@@ -153,6 +154,87 @@ __global__ __launch_bounds__(256) void copy_rows16_kernel(uint4* __restrict__ ds
     }
 }
 
+// Same dtype, a transpose: the destination's innermost axis l is strided in the source while
+// another axis j is unit-stride there (a transposed view made contiguous, as dot() does with
+// B^T).  The (j, l) plane is copied in VE x VE register blocks (VE = elements per 16 bytes):
+// lane (lb = lane % 8, jb = lane / 8) of wave w loads VE source rows (l .. l + VE - 1) of VE
+// consecutive j, transposes the block in registers and stores VE destination rows (j ..) of VE
+// consecutive l, so 8 lanes cover 128 contiguous bytes on both sides.  Further axes are the
+// batch (blockIdx.z).  Extents, strides and pointers are whole 16-byte units on this path.
+struct TransDesc {
+    int nb;                                 // batch axes
+    FastDiv bshape[MX_MAX_DIMS];
+    uint32_t bsd[MX_MAX_DIMS], bss[MX_MAX_DIMS];
+    uint32_t J, L;                          // plane extents: source-contiguous j, destination-contiguous l
+    uint32_t sdj, ssl;                      // destination stride of j, source stride of l
+};
+
+template <typename S>
+__global__ __launch_bounds__(256) void copy_transpose16_kernel(S* __restrict__ dst, const S* __restrict__ src,
+                                                               TransDesc d) {
+    constexpr int VE = 16 / sizeof(S);
+    struct alignas(16) V { S v[VE]; };
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t l = blockIdx.y * (8 * VE) + (lane & 7) * VE;
+    const uint32_t j = (blockIdx.x * 32 + wave * 8 + (lane >> 3)) * VE;
+    if (j >= d.J || l >= d.L) return;
+    uint32_t b = blockIdx.z;
+    uint64_t od = 0, os = 0;
+    for (int k = d.nb - 1; k >= 0; --k) {
+        const uint32_t q = d.bshape[k].div(b);
+        const uint32_t idx = b - q * d.bshape[k].d;
+        b = q;
+        od += (uint64_t)idx * d.bsd[k];
+        os += (uint64_t)idx * d.bss[k];
+    }
+    const S* s0 = src + os + j;
+    V v[VE];
+#pragma unroll
+    for (int i = 0; i < VE; i++) v[i] = *reinterpret_cast<const V*>(s0 + (uint64_t)(l + i) * d.ssl);
+    S* d0 = dst + od + l;
+#pragma unroll
+    for (int jj = 0; jj < VE; jj++) {
+        V w;
+#pragma unroll
+        for (int i = 0; i < VE; i++) w.v[i] = v[i].v[jj];
+        *reinterpret_cast<V*>(d0 + (uint64_t)(j + jj) * d.sdj) = w;
+    }
+}
+
+// Sets up the transpose path; false when the copy is not a same-dtype aligned transpose.
+template <typename S>
+bool launch_transpose16(int cdims, const uint32_t* shape, const uint32_t* sDst, const uint32_t* sSrc, void* dst,
+                        const void* src, hipStream_t st) {
+    constexpr uint32_t VE = 16 / sizeof(S);
+    const int last = cdims - 1;
+    if (cdims < 2 || sDst[last] != 1 || sSrc[last] == 1) return false;
+    int jax = -1;
+    for (int k = last - 1; k >= 0; --k)
+        if (sSrc[k] == 1 && shape[k] > 1) { jax = k; break; }
+    if (jax < 0) return false;
+    if ((uintptr_t)dst % 16 || (uintptr_t)src % 16) return false;
+    TransDesc d{};
+    d.J = shape[jax];
+    d.L = shape[last];
+    d.sdj = sDst[jax];
+    d.ssl = sSrc[last];
+    if (d.J % VE || d.L % VE || d.sdj % VE || d.ssl % VE) return false;
+    uint64_t batch = 1;
+    for (int k = 0; k < last; k++) {
+        if (k == jax) continue;
+        if (sDst[k] % VE || sSrc[k] % VE) return false;
+        d.bshape[d.nb] = FastDiv(shape[k]);
+        d.bsd[d.nb] = sDst[k];
+        d.bss[d.nb] = sSrc[k];
+        d.nb++;
+        batch *= shape[k];
+    }
+    if (batch > 65535) return false;
+    const dim3 grid((d.J + 32 * VE - 1) / (32 * VE), (d.L + 8 * VE - 1) / (8 * VE), (uint32_t)batch);
+    hipLaunchKernelGGL((copy_transpose16_kernel<S>), grid, dim3(256), 0, st, (S*)dst, (const S*)src, d);
+    return true;
+}
+
 template <typename F>
 bool dispatch_pair(int dd, int sd, F&& f) {
     bool ok = false;
@@ -205,6 +287,16 @@ extern "C" int mx_launch_copy_strided(int dst_dtype, int src_dtype, int cdims, c
             const uint32_t blocks = (uint32_t)(want < 65536 ? want : 65536);
             hipLaunchKernelGGL(copy_rows16_kernel, dim3(blocks), dim3(256), 0, st, (uint4*)dst, (const uint4*)src,
                                chunks, (uint32_t)es, d);
+            MX_HIP(hipGetLastError());
+            return MX_OK;
+        }
+    }
+    if (dst_dtype == src_dtype) {
+        bool done = false;
+        if (es == 4) done = launch_transpose16<uint32_t>(cdims, shape, sDst, sSrc, dst, src, st);
+        else if (es == 2) done = launch_transpose16<uint16_t>(cdims, shape, sDst, sSrc, dst, src, st);
+        else if (es == 8) done = launch_transpose16<uint64_t>(cdims, shape, sDst, sSrc, dst, src, st);
+        if (done) {
             MX_HIP(hipGetLastError());
             return MX_OK;
         }

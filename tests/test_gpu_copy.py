@@ -113,3 +113,29 @@ def test_rank0_and_empty(mx, orc):
     assert Y.download(np.int32, 1)[0] == 3
     mx.launch_copy_strided(mx.INT32, mx.FLOAT32, ([0], [1], [1]), Y.ptr, X.ptr)   # nothing to do
     mx.sync()
+
+
+@pytest.mark.parametrize("shape,perm", [
+    ([512, 4096], (1, 0)),               # an activation transpose of the MLP step
+    ([136, 200], (1, 0)),                # ragged grid in both plane axes
+    ([3, 256, 96], (0, 2, 1)),           # batched transpose (batch on blockIdx.z)
+    ([2, 40, 3, 64], (0, 3, 1, 2)),      # batch axes on both sides of the plane
+    ([10, 4096], (1, 0)),                # unaligned extent: scalar kernel
+])
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "INT64", "UINT16", "INT32"])
+def test_transposes(mx, orc, shape, perm, dt):
+    """Same-dtype transposed copies (dot()'s B^T): 16-byte register-block transposes when
+    extents and strides are whole 16-byte units, the scalar kernel otherwise."""
+    rng = np.random.default_rng(2)
+    x = values(dt, int(np.prod(shape)), rng)
+    st = contiguous_strides(shape)
+    vshape = [shape[p] for p in perm]
+    vst = [st[p] for p in perm]
+    desc = mx.collapse_dims2(vshape, contiguous_strides(vshape), vst)
+    X = mx.DeviceBuffer.from_numpy(x)
+    Y = mx.DeviceBuffer(x.nbytes)
+    code = getattr(mx, dt)
+    mx.launch_copy_strided(code, code, desc, Y.ptr, X.ptr)
+    mx.sync()
+    got = Y.download(x.dtype, x.size)
+    assert np.array_equal(bits(got), bits(x.reshape(shape).transpose(perm).ravel()))
