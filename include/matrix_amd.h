@@ -111,6 +111,21 @@ int mx_launch_reduce(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduc
                      void* out, const void* in, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* R = A op B exactly as mx_launch_bcast_binary, and out[r] = red_op over R[r * n .. r * n + n)
+ * (the values as stored in R; R must be contiguous, n must divide the result's size and
+ * n * sizeof(dtype) <= 16384).  out is contiguous, one element per row (int32 for ARGMAX /
+ * ARGMIN, the dtype otherwise); results equal mx_launch_bcast_binary followed by
+ * mx_launch_reduce over the rows bit for bit, except that float sums may round differently
+ * (another fixed summation order).  No counterpart in the reference: the graph layer's fusion of
+ * a broadcast node (add/sub/mul/divide/max/min_gpu_brodcasted, Matrix.mm:7709-8238) with a
+ * Sum / Max / Min / ArgMax / ArgMin over its last axis (Matrix.mm:15099-15208,
+ * Matrix.mm:14812-15059, Matrix.mm:16182-16458), which writes R and reduces it from registers.
+ * Float dtypes with Sum / Max / Min run fused; the rest run the two kernels in turn.
+ * MX_ERR_UNSUPPORTED when those rows would need a split reduction's workspace. */
+int mx_launch_bcast_binary_reduce_rows(int op, int red_op, int dtype, int cdims, const uint32_t* shape,
+                                       const uint32_t* sR, const uint32_t* sA, const uint32_t* sB, uint32_t n,
+                                       void* R, const void* A, const void* B, void* out, void* stream);
+
 /* C[b, m, n] = sum_k A[b, m, k] * Bt[b, n, k].  Replaces dot_gpu / batched_dot_gpu
  * (Matrix.mm:7198-7291).  The arrays are exactly CollapsedDims_3 from collapse_dims_matmul
  * (Mods/Utils.mm:204-252): shapeC = [batch..., M, N], sA / sBt / sC per axis, whose last

@@ -89,6 +89,8 @@ _SIGS = {
     "mx_launch_conv_nd": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _ip, _ip, _ip, _ip,
                            _i, _i, _vp, _vp, _vp, _vp, _sz, _vp], _i),
     "mx_launch_copy_strided": ([_i, _i, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp], _i),
+    "mx_launch_bcast_binary_reduce_rows": ([_i, _i, _i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp,
+                                            _vp], _i),
 }
 
 for _name, (_args, _res) in _SIGS.items():
@@ -292,6 +294,27 @@ def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=
     shape, sOut, sIn = desc
     check(lib.mx_launch_reduce(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn),
                                int(out), int(inp), int(workspace), workspace_bytes, stream))
+
+
+def launch_bcast_binary_reduce_rows(op, red_op, dtype, desc, n, R, A, B, out, stream=None):
+    """R = A op B (desc as for launch_bcast_binary) and out[r] = red_op over R's rows of n."""
+    shape, sA, sB, sR = desc
+    check(lib.mx_launch_bcast_binary_reduce_rows(op, red_op, dtype, len(shape), u32(shape), u32(sR), u32(sA),
+                                                 u32(sB), n, int(R), int(A), int(B), int(out), stream))
+
+
+def prepare_bcast_binary_reduce_rows(op, red_op, dtype, desc, n, stream=None):
+    """launch_bcast_binary_reduce_rows with its descriptor converted once: returns launch(R, A, B, out)."""
+    shape, sA, sB, sR = desc
+    fn = lib.mx_launch_bcast_binary_reduce_rows
+    head = (op, red_op, dtype, len(shape), u32(shape), u32(sR), u32(sA), u32(sB), n)
+
+    def launch(R, A, B, out):
+        status = fn(*head, R, A, B, out, stream)
+        if status != OK:
+            raise MatrixAMDError(status, last_error())
+
+    return launch
 
 
 def prepare_bcast_binary(op, dtype, desc, stream=None):

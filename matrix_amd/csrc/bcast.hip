@@ -13,56 +13,10 @@
 // (Mods/Utils.mm:169-202).  When the innermost collapsed axis is unit-stride in the output
 // and unit- or zero-stride in each operand, one thread moves 16 bytes per operand with
 // 128-bit loads and stores; otherwise a scalar kernel gathers with the full strides.
-#include "common.hpp"
+#include "elementwise.hpp"
 
 namespace mx {
 namespace {
-
-template <int DT, int OP>
-struct BinOp {
-    using Tr = dt_traits<DT>;
-    using S = typename Tr::S;
-    __device__ __forceinline__ static S apply(S a, S b) {
-        if constexpr (Tr::is_float) {
-            float x = Tr::ld(a), y = Tr::ld(b);
-            if constexpr (OP == MX_OP_ADD) return Tr::st(x + y);
-            else if constexpr (OP == MX_OP_SUB) return Tr::st(x - y);
-            else if constexpr (OP == MX_OP_MUL) return Tr::st(x * y);
-            else if constexpr (OP == MX_OP_DIV) return Tr::st(x / y);
-            else if constexpr (OP == MX_OP_MAX) return (x < y) ? b : a;
-            else if constexpr (OP == MX_OP_MIN) return (y < x) ? b : a;
-            else return (x == y) ? Tr::st(1.0f) : Tr::st(0.0f);
-        } else if constexpr (DT == MX_BOOL) {
-            int x = a, y = b;
-            if constexpr (OP == MX_OP_ADD) return (S)((x + y) != 0);
-            else if constexpr (OP == MX_OP_SUB) return (S)((x - y) != 0);
-            else if constexpr (OP == MX_OP_MUL) return (S)((x * y) != 0);
-            else if constexpr (OP == MX_OP_DIV) return (S)(y == 0 ? 0 : ((x / y) != 0));
-            else if constexpr (OP == MX_OP_MAX) return (x < y) ? b : a;
-            else if constexpr (OP == MX_OP_MIN) return (y < x) ? b : a;
-            else return (S)(x == y ? 1 : 0);
-        } else {
-            // wrap-around arithmetic in an unsigned type at least 32 bits wide
-            using U = std::conditional_t<(sizeof(S) <= 4), uint32_t, uint64_t>;
-            if constexpr (OP == MX_OP_ADD) return (S)((U)a + (U)b);
-            else if constexpr (OP == MX_OP_SUB) return (S)((U)a - (U)b);
-            else if constexpr (OP == MX_OP_MUL) return (S)((U)a * (U)b);
-            else if constexpr (OP == MX_OP_DIV) {
-                if (b == 0) return (S)0;
-                if constexpr (Tr::is_signed) {
-                    using W = std::conditional_t<(sizeof(S) <= 4), int32_t, int64_t>;
-                    W x = a, y = b;
-                    if (y == -1) return (S)(0 - (U)x);      // MIN / -1 wraps to MIN
-                    return (S)(x / y);
-                } else {
-                    return (S)((U)a / (U)b);
-                }
-            } else if constexpr (OP == MX_OP_MAX) return (a < b) ? b : a;
-            else if constexpr (OP == MX_OP_MIN) return (b < a) ? b : a;
-            else return (S)(a == b ? 1 : 0);
-        }
-    }
-};
 
 constexpr int kMaxOuter = MX_MAX_DIMS - 1;
 

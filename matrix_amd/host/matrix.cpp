@@ -257,11 +257,20 @@ struct ViewPrim : Primitive {
 };
 
 // Broadcast binary op (and Equal): out = a op b with NumPy broadcasting.
+// When a reduction over this node's last axis is compiled against it (ReducePrim::compile), the
+// node also produces that reduction: execute() launches mx_launch_bcast_binary_reduce_rows, which
+// writes this node's result and the reduction's output together, and counts the fused runs so the
+// reduction knows when its output is already current.  The reduction's storage is held weakly
+// (the reduction node holds this one, not the other way round).
 struct BinaryPrim : Primitive {
     int op;
     matrix a, b;
     uint32_t cd = 0;
     uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sR[MX_MAX_DIMS];
+    std::weak_ptr<matrix_amd::Storage> fused_out;   // the fused reduction's output
+    int fused_red_op = -1;
+    uint32_t fused_n = 0;
+    uint64_t fused_runs = 0;
     BinaryPrim(int o, matrix x, matrix y) : op(o), a(std::move(x)), b(std::move(y)) {}
     const char* name() const override {
         static const char* n[] = {"Add", "Sub", "Mul", "Divide", "Max", "Min", "Equal"};
@@ -277,6 +286,13 @@ struct BinaryPrim : Primitive {
         check(mx_collapse_dims3(os, b1t, b2t, ost, out.dims, kCap, cs, sA, sB, sR, &cd), "collapse_dims");
     }
     void execute(const matrix& out) override {
+        if (auto red = fused_out.lock(); red && red->dev && fused_red_op >= 0) {
+            check(mx_launch_bcast_binary_reduce_rows(op, fused_red_op, (int)a.type, (int)cd, cs, sR, sA, sB, fused_n,
+                                                     dptr(out), dptr(a), dptr(b), red->dev, nullptr),
+                  std::string("launch ") + name() + " + reduction");
+            fused_runs++;
+            return;
+        }
         check(mx_launch_bcast_binary(op, (int)a.type, (int)cd, cs, sR, sA, sB, dptr(out), dptr(a), dptr(b), nullptr),
               std::string("launch ") + name());
     }
@@ -313,6 +329,8 @@ struct ReducePrim : Primitive {
     uint32_t cd = 0, rstride = 0, n = 0;
     uint32_t cs[MX_MAX_DIMS], sOut[MX_MAX_DIMS], sIn[MX_MAX_DIMS];
     DevBuf ws;
+    BinaryPrim* producer = nullptr;     // fused into this broadcast node (kept alive by `in`)
+    uint64_t seen_runs = 0;
     ReducePrim(int o, matrix x, int ax, bool kd) : op(o), in(std::move(x)), axis(ax), keepdims(kd) {}
     const char* name() const override {
         static const char* nm[] = {"Sum", "Max", "Min", "ArgMax", "ArgMin"};
@@ -320,7 +338,7 @@ struct ReducePrim : Primitive {
     }
     uint32_t num_inputs() const override { return 1; }
     matrix& input_at(uint32_t) override { return in; }
-    void compile(const matrix&) override {
+    void compile(const matrix& out) override {
         // the output is contiguous; keepdims does not change its layout
         std::vector<size_m> oshape;
         for (uint32_t i = 0; i < in.dims; i++)
@@ -334,8 +352,25 @@ struct ReducePrim : Primitive {
         size_t bytes = 0;
         check(mx_reduce_workspace_bytes(op, (int)in.type, rstride, n, (int)cd, cs, sOut, sIn, &bytes), "reduce workspace");
         if (bytes) ws.reserve(bytes);
+        try_fuse(out);
+    }
+    // Fuse into the producing broadcast node when this reduces its last axis (rows of at most
+    // 16 KiB, no split workspace) and the producer has no fused reduction yet.
+    void try_fuse(const matrix& out) {
+        auto* bp = dynamic_cast<BinaryPrim*>(in.tape.get());
+        if (!bp || bp->fused_red_op >= 0 || in.dims == 0 || axis != (int)in.dims - 1 || ws.bytes || n == 0) return;
+        if (!in.is_contiguous() || in.offset != 0 || (uint64_t)n * dtype_size(in.type) > 16384) return;
+        bp->fused_out = out.storage;
+        bp->fused_red_op = op;
+        bp->fused_n = n;
+        producer = bp;
+        seen_runs = bp->fused_runs;
     }
     void execute(const matrix& out) override {
+        if (producer && producer->fused_runs != seen_runs) {   // the producer already wrote this output
+            seen_runs = producer->fused_runs;
+            return;
+        }
         check(mx_launch_reduce(op, (int)in.type, rstride, n, (int)cd, cs, sOut, sIn, dptr(out), dptr(in), ws.p, ws.bytes,
                                nullptr), std::string("launch ") + name());
     }

@@ -10,6 +10,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <random>
 #include <string>
 #include <vector>
@@ -144,6 +145,65 @@ CASE(gpu_add_then_rowsum) {
         double ref = 0, mag = 0;
         for (size_t j = 0; j < Cc; j++) { ref += (double)cg[r * Cc + j]; mag += std::fabs(cg[r * Cc + j]); }
         EXPECT(std::fabs(sg[r] - ref) <= 1e-4 * mag, "row sum beyond 1e-4 of sum|x|");
+    }
+}
+
+// A reduction over a broadcast node's last axis is fused into that node's launch: the results
+// stay right when the graph is re-executed after a leaf changes, when a second reduction of the
+// same node is added (not fused), when only the reduction is executed, and when a reduction is
+// attached to a node that has already run.
+CASE(gpu_fused_reduction_lifecycle) {
+    const size_m R = 512, Cc = 768;
+    auto av = randn((size_t)R * Cc, 20);
+    auto bv = randu(Cc, 21, -1.f, 1.f);
+    matrix a = matrix::from_host<float>({R, Cc}, av);
+    matrix b = matrix::from_host<float>({1, Cc}, bv);
+    matrix c = a * b;
+    matrix s = c.sum(1);                       // fused into c
+    matrix m = c.max(1);                       // second reduction of c: its own launch
+    std::vector<matrix> outs{c, s, m};
+    auto check = [&](const std::vector<float>& aa, const char* when) {
+        auto cg = c.to_host<float>();
+        auto sg = s.to_host<float>();
+        auto mg = m.to_host<float>();
+        for (size_t r = 0; r < R; r++) {
+            double ref = 0, mag = 0;
+            float mx = -3.4028234663852886e38f;
+            for (size_t j = 0; j < Cc; j++) {
+                const float v = aa[r * Cc + j] * bv[j];
+                EXPECT(cg[r * Cc + j] == v, std::string("product not exact ") + when);
+                ref += v; mag += std::fabs(v);
+                if (mx < v) mx = v;
+            }
+            EXPECT(std::fabs(sg[r] - ref) <= 1e-4 * mag, std::string("fused row sum ") + when);
+            EXPECT(mg[r] == mx, std::string("row max ") + when);
+        }
+    };
+    matrix::compile_gpu(outs);
+    matrix::execute_gpu(outs);
+    check(av, "first run");
+    for (int it = 0; it < 2; it++) {           // new leaf values, re-executed
+        auto av2 = randn((size_t)R * Cc, 30 + it);
+        std::memcpy(a.host_data(), av2.data(), av2.size() * sizeof(float));
+        a.mark_changed();
+        matrix::clear_trace_checks(outs);
+        matrix::execute_gpu(outs);
+        check(av2, "after mark_changed");
+        av = av2;
+    }
+    std::vector<matrix> only_s{s};             // only the reduction: the producer runs (fused) first
+    matrix::clear_trace_checks(only_s);
+    matrix::execute_gpu(only_s);
+    check(av, "executing the reduction alone");
+    matrix s2 = c.sum(1);                       // attached after c ran: computed by its own launch
+    std::vector<matrix> late{s2};
+    matrix::eval(late);
+    auto s2g = s2.to_host<float>();
+    auto sg = s.to_host<float>();
+    for (size_t r = 0; r < R; r++) {
+        double mag = 0;
+        for (size_t j = 0; j < Cc; j++) mag += std::fabs(av[r * Cc + j] * bv[j]);
+        EXPECT(std::fabs(s2g[r] - sg[r]) <= 2e-4 * mag, "late reduction");
     }
 }
 
@@ -370,6 +430,7 @@ int main(int argc, char** argv) {
         run("grad_graph_structure", grad_graph_structure);
     } else {
         run("gpu_add_then_rowsum", gpu_add_then_rowsum);
+        run("gpu_fused_reduction_lifecycle", gpu_fused_reduction_lifecycle);
         run("gpu_reductions_and_views", gpu_reductions_and_views);
         run("gpu_dot_batched_broadcast", gpu_dot_batched_broadcast);
         run("gpu_conv2d_nchw_views", gpu_conv2d_nchw_views);
