@@ -75,6 +75,14 @@ int mx_hip_memset(void* dst, int value, size_t bytes, void* stream);
 int mx_hip_stream_for_thread(void** stream);
 int mx_hip_sync(void* stream);
 
+/* Further streams for independent work (no counterpart in the reference, whose encoder is one
+ * in-order queue per thread, GPUManager.h:57-58): a caller that runs independent nodes
+ * concurrently creates streams, orders them with events (record on one, wait on another), and
+ * destroys them when done.  Streams have the default priority. */
+int mx_hip_stream_create(void** stream);
+int mx_hip_stream_destroy(void* stream);
+int mx_hip_stream_wait_event(void* stream, void* event);
+
 /* Timing (the reference's Timer, Mods/Utils.h:316-335, but on the device clock). */
 int mx_hip_event_create(void** event);
 int mx_hip_event_destroy(void* event);

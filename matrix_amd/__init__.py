@@ -71,6 +71,9 @@ _SIGS = {
     "mx_hip_memset": ([_vp, _i, _sz, _vp], _i),
     "mx_hip_stream_for_thread": ([ctypes.POINTER(_vp)], _i),
     "mx_hip_sync": ([_vp], _i),
+    "mx_hip_stream_create": ([ctypes.POINTER(_vp)], _i),
+    "mx_hip_stream_destroy": ([_vp], _i),
+    "mx_hip_stream_wait_event": ([_vp, _vp], _i),
     "mx_hip_event_create": ([ctypes.POINTER(_vp)], _i),
     "mx_hip_event_destroy": ([_vp], _i),
     "mx_hip_event_record": ([_vp, _vp], _i),
@@ -189,6 +192,33 @@ class DeviceBuffer:
             self.free()
         except Exception:
             pass
+
+
+class Stream:
+    """An extra stream (mx_hip_stream_create); pass .ptr as a launch's stream."""
+
+    def __init__(self):
+        init()
+        p = ctypes.c_void_p()
+        check(lib.mx_hip_stream_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def wait(self, event: "Event") -> None:
+        check(lib.mx_hip_stream_wait_event(self.ptr, event.ptr))
+
+    def sync(self) -> None:
+        check(lib.mx_hip_sync(self.ptr))
+
+    def __del__(self):
+        try:
+            lib.mx_hip_stream_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+def wait_event(event: "Event", stream=None) -> None:
+    """Make `stream` (default: the calling thread's stream) wait for `event`."""
+    check(lib.mx_hip_stream_wait_event(stream, event.ptr))
 
 
 class Event:

@@ -187,6 +187,41 @@ int mx_hip_stream_for_thread(void** stream) {
     return MX_OK;
 }
 
+// Extra streams for callers that run independent nodes concurrently (no counterpart in the
+// reference, whose encoder is one in-order queue per thread).  Default priority, non-blocking.
+int mx_hip_stream_create(void** stream) {
+    if (!stream) return fail(MX_ERR_INVALID_ARG, "mx_hip_stream_create: null pointer");
+    if (g_device.load() < 0) return fail(MX_ERR_NOT_INITIALIZED, "mx_hip_init() was not called");
+    hipStream_t s = nullptr;
+    MX_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = (void*)s;
+    return MX_OK;
+}
+
+int mx_hip_stream_destroy(void* stream) {
+    if (!stream) return MX_OK;
+    hipStream_t s = (hipStream_t)stream;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);     // the stream's split-K scratch, if any
+        auto it = g_scratch.find(s);
+        if (it != g_scratch.end()) {
+            MX_HIP(hipStreamSynchronize(s));
+            if (it->second.ptr) MX_HIP(hipFree(it->second.ptr));
+            g_scratch.erase(it);
+        }
+    }
+    MX_HIP(hipStreamDestroy(s));
+    return MX_OK;
+}
+
+int mx_hip_stream_wait_event(void* stream, void* event) {
+    if (!event) return fail(MX_ERR_INVALID_ARG, "mx_hip_stream_wait_event: null event");
+    hipStream_t s;
+    if (!resolve_stream(stream, &s)) return MX_ERR_NOT_INITIALIZED;
+    MX_HIP(hipStreamWaitEvent(s, (hipEvent_t)event, 0));
+    return MX_OK;
+}
+
 int mx_hip_sync(void* stream) {
     hipStream_t s;
     if (!resolve_stream(stream, &s)) return MX_ERR_NOT_INITIALIZED;

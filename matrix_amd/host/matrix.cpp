@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <mutex>
 #include <numeric>
 #include <unordered_map>
@@ -288,12 +289,12 @@ struct BinaryPrim : Primitive {
     void execute(const matrix& out) override {
         if (auto red = fused_out.lock(); red && red->dev && fused_red_op >= 0) {
             check(mx_launch_bcast_binary_reduce_rows(op, fused_red_op, (int)a.type, (int)cd, cs, sR, sA, sB, fused_n,
-                                                     dptr(out), dptr(a), dptr(b), red->dev, nullptr),
+                                                     dptr(out), dptr(a), dptr(b), red->dev, stream),
                   std::string("launch ") + name() + " + reduction");
             fused_runs++;
             return;
         }
-        check(mx_launch_bcast_binary(op, (int)a.type, (int)cd, cs, sR, sA, sB, dptr(out), dptr(a), dptr(b), nullptr),
+        check(mx_launch_bcast_binary(op, (int)a.type, (int)cd, cs, sR, sA, sB, dptr(out), dptr(a), dptr(b), stream),
               std::string("launch ") + name());
     }
     std::vector<matrix> vjp(matrix& g) override {
@@ -372,7 +373,7 @@ struct ReducePrim : Primitive {
             return;
         }
         check(mx_launch_reduce(op, (int)in.type, rstride, n, (int)cd, cs, sOut, sIn, dptr(out), dptr(in), ws.p, ws.bytes,
-                               nullptr), std::string("launch ") + name());
+                               stream), std::string("launch ") + name());
     }
     std::vector<matrix> vjp(matrix& g) override {
         if (op != MX_RED_SUM) throw std::logic_error(std::string("matrix: no vjp for ") + name());
@@ -403,7 +404,7 @@ struct DotPrim : Primitive {
         }
     }
     void execute(const matrix& out) override {
-        check(mx_launch_batched_matmul((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a), dptr(bt), nullptr),
+        check(mx_launch_batched_matmul((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a), dptr(bt), stream),
               "launch Dot");
     }
     std::vector<matrix> vjp(matrix& g) override {
@@ -433,7 +434,7 @@ struct CopyPrim : Primitive {
         (void)out;
     }
     void execute(const matrix& out) override {
-        check(mx_launch_copy_strided((int)out.type, (int)in.type, (int)cd, cs, sD, sS, dptr(out), dptr(in), nullptr),
+        check(mx_launch_copy_strided((int)out.type, (int)in.type, (int)cd, cs, sD, sS, dptr(out), dptr(in), stream),
               "launch AsType");
     }
     std::vector<matrix> vjp(matrix& g) override { return {g.astype(in.type)}; }
@@ -465,7 +466,7 @@ struct ConvPrim : Primitive {
     void execute(const matrix& out) override {
         check(mx_launch_conv_nd((int)in.type, (int)in.dims - 2, ishape.data(), kshape.data(), oshape.data(), ist.data(),
                                 kst.data(), ost.data(), pad_lo.data(), stride.data(), dil.data(), dil_lhs.data(), groups,
-                                flip ? 1 : 0, dptr(out), dptr(in), dptr(k), ws.p, ws_bytes, nullptr),
+                                flip ? 1 : 0, dptr(out), dptr(in), dptr(k), ws.p, ws_bytes, stream),
               "launch Convolve");
     }
     std::vector<matrix> vjp(matrix&) override { throw std::logic_error("matrix: no vjp for Convolve"); }
@@ -697,16 +698,117 @@ void compile_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {
     }
 }
 
-void execute_node(const matrix& m) {
+// ------------------------------------------------------------------ the executor
+// execute_gpu launches the graph's unevaluated nodes in topological order.  The pending nodes
+// split into independent parts (weakly connected components of their data dependencies: leaves
+// and nodes evaluated by an earlier execute do not connect anything); each part runs on one
+// stream, and the parts take the executor's streams round-robin (two by default;
+// MATRIX_AMD_STREAMS=1 gives the reference's single in-order queue).  Independent reductions of
+// one input thus overlap -- one kernel's tail with another's start -- while a connected graph
+// such as a training step stays on one stream and needs no cross-stream waits.  Every stream
+// then joins the calling thread's stream, which execute waits on once, as execute_metal commits
+// and waits (Matrix.mm:8452-8475).
+struct Executor {
+    std::vector<void*> streams;     // [0] is the thread's stream
+    std::vector<void*> events;
+    int count = 0;
+    Executor() {
+        const char* env = std::getenv("MATRIX_AMD_STREAMS");
+        count = env ? std::atoi(env) : 2;
+        if (count < 1) count = 1;
+        if (count > 8) count = 8;
+    }
+    // The streams and events live until the process ends: releasing them from a thread-exit
+    // destructor could run after the HIP runtime has shut down.
+    void* stream(int i) {
+        if (streams.empty()) {
+            void* s0 = nullptr;
+            check(mx_hip_stream_for_thread(&s0), "executor stream");
+            streams.push_back(s0);
+        }
+        while ((int)streams.size() <= i) {
+            void* s = nullptr;
+            check(mx_hip_stream_create(&s), "executor stream");
+            streams.push_back(s);
+        }
+        return streams[i];
+    }
+    void* event(int i) {
+        while ((int)events.size() <= i) {
+            void* e = nullptr;
+            check(mx_hip_event_create(&e), "executor event");
+            events.push_back(e);
+        }
+        return events[i];
+    }
+};
+
+Executor& executor() {
+    thread_local Executor ex;
+    return ex;
+}
+
+void collect(const matrix& m, std::vector<matrix>& nodes, std::unordered_map<const Primitive*, int>& index) {
     if (!m.tape) {
         if (m.storage->dev_stale) m.storage->upload();      // leaf written on the host
         return;
     }
-    if (m.tape->evaluated) return;
-    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) execute_node(m.tape->input_at(i));
+    if (m.tape->evaluated || index.count(m.tape.get())) return;
     if (!m.tape->compiled) throw std::logic_error("matrix: execute before compile");
-    m.tape->execute(m);
-    m.tape->evaluated = true;
+    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) collect(m.tape->input_at(i), nodes, index);
+    index[m.tape.get()] = (int)nodes.size();
+    nodes.push_back(m);
+}
+
+int find_root(std::vector<int>& parent, int i) {
+    while (parent[i] != i) i = parent[i] = parent[parent[i]];
+    return i;
+}
+
+void run_graph(std::vector<matrix>& ms) {
+    std::vector<matrix> nodes;
+    std::unordered_map<const Primitive*, int> index;
+    for (auto& m : ms) collect(m, nodes, index);
+    std::vector<int> parent(nodes.size());
+    std::iota(parent.begin(), parent.end(), 0);
+    for (size_t i = 0; i < nodes.size(); i++) {         // parts: union with every pending input
+        Primitive* p = nodes[i].tape.get();
+        for (uint32_t j = 0; j < p->num_inputs(); j++) {
+            const matrix& in = p->input_at(j);
+            if (!in.tape) continue;
+            auto it = index.find(in.tape.get());
+            if (it == index.end()) continue;
+            const int a = find_root(parent, (int)i), b = find_root(parent, it->second);
+            if (a != b) parent[std::max(a, b)] = std::min(a, b);
+        }
+    }
+    Executor& ex = executor();
+    const int K = ex.count;
+    std::unordered_map<int, int> part_stream;
+    std::vector<bool> used(K, false);
+    used[0] = true;
+    for (size_t i = 0; i < nodes.size(); i++) {
+        Primitive* p = nodes[i].tape.get();
+        if (!p->is_view()) {
+            const int root = find_root(parent, (int)i);
+            auto it = part_stream.find(root);
+            const int k = it != part_stream.end() ? it->second : (int)(part_stream.size() % K);
+            if (it == part_stream.end()) part_stream.emplace(root, k);
+            used[k] = true;
+            p->stream = ex.stream(k);
+            p->execute(nodes[i]);
+        }
+        p->evaluated = true;
+    }
+    void* s0 = ex.stream(0);
+    int nev = 0;
+    for (int k = 1; k < K; k++) {                        // join into the thread's stream
+        if (!used[k]) continue;
+        void* e = ex.event(nev++);
+        check(mx_hip_event_record(e, ex.stream(k)), "event record");
+        check(mx_hip_stream_wait_event(s0, e), "stream wait");
+    }
+    check(mx_hip_sync(s0), "execute");
 }
 
 void clear_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {
@@ -722,10 +824,7 @@ void matrix::compile_gpu(std::vector<matrix>& ms) {
     std::unordered_set<const Primitive*> seen;
     for (auto& m : ms) compile_node(m, seen);
 }
-void matrix::execute_gpu(std::vector<matrix>& ms) {
-    for (auto& m : ms) execute_node(m);
-    check(mx_hip_sync(nullptr), "execute");
-}
+void matrix::execute_gpu(std::vector<matrix>& ms) { run_graph(ms); }
 void matrix::clear_trace_checks(std::vector<matrix>& ms) {
     std::unordered_set<const Primitive*> seen;
     for (auto& m : ms) clear_node(m, seen);

@@ -218,4 +218,5 @@ public:
     virtual std::vector<matrix> vjp(matrix& grad_out) = 0;
     bool compiled = false;
     bool evaluated = false;
+    void* stream = nullptr;        // the stream execute() launches on (set by the executor)
 };
