@@ -387,9 +387,11 @@ CASE(gpu_mlp_training_step_compile_once) {
     std::vector<matrix> all = grads;
     all.push_back(loss);
     matrix::compile_gpu(all);
-    for (int iter = 0; iter < 3; iter++) {
-        if (iter == 2) {           // new inputs through the compiled graph: host write + mark_changed
-            auto x2 = randn((size_t)s.B * s.D0, 99);
+    // executes 0 (eager), 1 (captured into a HIP graph), 2-4 (replays of it); new inputs through
+    // the compiled graph before executes 2 and 4: host write + mark_changed
+    for (int iter = 0; iter < 5; iter++) {
+        if (iter == 2 || iter == 4) {
+            auto x2 = randn((size_t)s.B * s.D0, 99 + iter);
             std::memcpy(x.host_data(), x2.data(), x2.size() * 4);
             x.mark_changed();
             xv = x2;
