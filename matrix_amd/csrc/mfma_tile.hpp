@@ -406,22 +406,33 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     // pair p + 2 and reads pair p + 1's first fragments under the remaining MFMAs.  Steady pairs
     // have no branches, so the compiler's own wait bookkeeping stays exact; sched_barrier(0)
     // fences keep each phase's instructions inside it.
+    // fp32 takes no interleave groups: with four MFMAs per slot the scheduler filled each group
+    // with four MFMAs on one accumulator (a dependent chain); left alone it alternates the 16
+    // accumulators.  It also reads the next pair's first fragments before issuing the DMA, since
+    // the compiler otherwise makes the reads after the DMA wait for it.  (fp32 main GEMM: 118 ->
+    // 127 TFLOP/s.)
     auto pair_steady = [&](auto s, uint32_t p) {
         using SN = std::integral_constant<int, 1 - decltype(s)::value>;
         constexpr int MF = kMfmaPerSlot<DT>;
         read_frags<DT, TM, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
         mma_step<DT, TM, WNT, 0, TM>(acc, f0);
-        interleave_even<DT, TM, WNT>();
+        if constexpr (DT != MX_FLOAT32) interleave_even<DT, TM, WNT>();
         __builtin_amdgcn_sched_barrier(0);
         mma_step<DT, TM, WNT, 0, H0>(acc, f1);
-        __builtin_amdgcn_sched_group_barrier(0x008, TM * WNT * MF, 0);
+        if constexpr (DT != MX_FLOAT32) __builtin_amdgcn_sched_group_barrier(0x008, TM * WNT * MF, 0);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmem<0>();
         ring_barrier();
-        dma_pair(s, p + 2);
-        read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+        if constexpr (DT == MX_FLOAT32) {
+            // fp32: the next pair's first fragments before the DMA, so no LDS read follows it
+            read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+            dma_pair(s, p + 2);
+        } else {
+            dma_pair(s, p + 2);
+            read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+        }
         mma_step<DT, TM, WNT, H0, TM>(acc, f1);
-        interleave_odd<DT, TM, WNT, BM, BN>();
+        if constexpr (DT != MX_FLOAT32) interleave_odd<DT, TM, WNT, BM, BN>();
         __builtin_amdgcn_sched_barrier(0);
     };
     // the last pairs: no DMA past the end, no barrier after the last
