@@ -30,6 +30,10 @@ namespace tile {
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef __bf16 b8v __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+// fp32 fragments are native 4-wide vectors: loaded through HIP's float4 struct, the LDS reads lost
+// the alias scopes that tell them apart from the DMA into the other slot, and the compiler then
+// made them wait for that DMA.
+typedef float f4v __attribute__((ext_vector_type(4)));
 
 constexpr int STEPB = 64;                 // bytes of K per row in one K step (one MFMA round)
 constexpr int ROWB = 2 * STEPB;           // bytes of one LDS row: a K pair, one 128-byte line
@@ -125,7 +129,7 @@ template <int TM, int WNT> struct Frags<MX_FLOAT16, TM, WNT> { static constexpr 
 template <int TM, int WNT> struct Frags<MX_BFLOAT16, TM, WNT> { static constexpr int KB = 2; b8v a[KB][TM], b[KB][WNT]; };
 template <int TM, int WNT> struct Frags<MX_FLOAT32, TM, WNT> {
     static constexpr int KB = 1;
-    float4 a[KB][TM][2], b[KB][WNT][2];
+    f4v a[KB][TM][2], b[KB][WNT][2];
 };
 
 template <int DT, int TM, int WNT, int HALF>
@@ -141,7 +145,7 @@ __device__ __forceinline__ void read_frags(Frags<DT, TM, WNT>& f, const char* la
             if constexpr (DT == MX_FLOAT32) {
 #pragma unroll
                 for (int u = 0; u < 2; u++)
-                    f.a[kb][t][u] = *reinterpret_cast<const float4*>(la + ra * ROWB + swz(ra, C0 + 2 * h + u) * 16);
+                    f.a[kb][t][u] = *reinterpret_cast<const f4v*>(la + ra * ROWB + swz(ra, C0 + 2 * h + u) * 16);
             } else {
                 using V = std::remove_reference_t<decltype(f.a[0][0])>;
                 f.a[kb][t] = *reinterpret_cast<const V*>(la + ra * ROWB + swz(ra, C0 + 2 * kb + h) * 16);
@@ -153,7 +157,7 @@ __device__ __forceinline__ void read_frags(Frags<DT, TM, WNT>& f, const char* la
             if constexpr (DT == MX_FLOAT32) {
 #pragma unroll
                 for (int u = 0; u < 2; u++)
-                    f.b[kb][t][u] = *reinterpret_cast<const float4*>(lb + rb * ROWB + swz(rb, C0 + 2 * h + u) * 16);
+                    f.b[kb][t][u] = *reinterpret_cast<const f4v*>(lb + rb * ROWB + swz(rb, C0 + 2 * h + u) * 16);
             } else {
                 using V = std::remove_reference_t<decltype(f.b[0][0])>;
                 f.b[kb][t] = *reinterpret_cast<const V*>(lb + rb * ROWB + swz(rb, C0 + 2 * kb + h) * 16);
@@ -162,10 +166,7 @@ __device__ __forceinline__ void read_frags(Frags<DT, TM, WNT>& f, const char* la
     }
 }
 
-__device__ __forceinline__ float f4_at(const float4 (&v)[2], int s) {
-    const float4& q = v[s >> 2];
-    switch (s & 3) { case 0: return q.x; case 1: return q.y; case 2: return q.z; default: return q.w; }
-}
+__device__ __forceinline__ float f4_at(const f4v (&v)[2], int s) { return v[s >> 2][s & 3]; }
 
 // MFMAs of the step for A tile rows I0 .. I1 - 1 of the wave's TM x WNT grid.  The Bt fragment
 // goes in the MFMA's first operand slot and the A fragment in the second, so the 32 x 32 result
