@@ -300,6 +300,17 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t
                              if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
                          return true;
                      }();
+    // fp32 B given N-major (Bt's K stride is B's row stride, its N stride 1): the tile kernel's
+    // N-major B slot, so dot() needs no transposed copy of B
+    bool nn = false;
+    if constexpr (DT == MX_FLOAT32)
+        nn = !vec && g.ka == 1 && g.ldb == 1 && g.kb % 4 == 0 && g.N % 4 == 0 && g.lda % 4 == 0 &&
+             (uint64_t)ts.bm * g.lda * 4 < (1ull << 32) && 32ull * g.kb * 4 < (1ull << 32) &&
+             (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0 && [&] {
+                 for (int d = 0; d < g.bd.n; d++)
+                     if (g.bd.sA[d] % 4 || g.bd.sB[d] % 4) return false;
+                 return true;
+             }();
     const tile::MatrixSrc::Geom geo{};
     const char* who = "mx_launch_batched_matmul";
     if (nsplit > 1 && per < 0xffffffffull) {
@@ -311,14 +322,19 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t
         gp.ksplit = ksplit;
         gp.ldc = g.N;
         gp.cn = 1;
-        rc = vec ? tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit)
-                 : tile::launch_tile_kernel<DT, false, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit);
+        if constexpr (DT == MX_FLOAT32)
+            if (nn) rc = tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc, true>(ts, gp, geo, P, A, Bt, st, who, nsplit);
+        if (!nn)
+            rc = vec ? tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit)
+                     : tile::launch_tile_kernel<DT, false, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit);
         if (rc) return rc;
         hipLaunchKernelGGL((splitk_sum_kernel<DT>), dim3((uint32_t)((per + 255) / 256)), dim3(256), 0, st, (S*)C,
                            (const float*)P, nsplit, g, FastDiv(g.N), FastDiv(g.M));
         MX_HIP(hipGetLastError());
         return MX_OK;
     }
+    if constexpr (DT == MX_FLOAT32)
+        if (nn) return tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc, true>(ts, g, geo, C, A, Bt, st, who);
     if (vec) return tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
     return tile::launch_tile_kernel<DT, false, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
 }

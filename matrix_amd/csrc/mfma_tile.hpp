@@ -199,6 +199,52 @@ __device__ __forceinline__ void mma_step(f16v (&acc)[TM][WNT], const Frags<DT, T
     }
 }
 
+// fp32 with Bt N-major (B given as [K, N], N contiguous -- dot()'s B without its transposed copy).
+// The B slot holds the pair's 32 K rows of BN floats.  The wave's WNT x 32 columns are read as 32
+// groups of WNT consecutive columns: lane (i = l % 32, h = l / 32) loads, for substep s, row 8 h + s
+// (the K offset the A fragment of lane half h holds, see Frags) and columns WNT i .. WNT i + WNT - 1,
+// and MFMA q of the substep takes element q as its row operand.  MFMA q thus covers the columns
+// n = WNT i + q: C^T row i of accumulator q is column WNT i + q, so a lane's WNT accumulators hold
+// WNT consecutive columns (one vector store in the epilogue).
+template <int TM, int WNT> struct FragsNN {
+    static constexpr int KB = 1;
+    typedef float bvec __attribute__((ext_vector_type(WNT)));
+    f4v a[1][TM][2];
+    bvec b[8];
+};
+
+template <int TM, int WNT, int BN, int HALF>
+__device__ __forceinline__ void read_frags_nn(FragsNN<TM, WNT>& f, const char* la, const char* lb, int wm, int wn,
+                                              int lane) {
+    using BV = typename FragsNN<TM, WNT>::bvec;
+    const int r32 = lane & 31, h = lane >> 5;
+    constexpr int C0 = HALF * STEP_CHUNKS;
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+        const int ra = wm * (TM * 32) + t * 32 + r32;
+#pragma unroll
+        for (int u = 0; u < 2; u++)
+            f.a[0][t][u] = *reinterpret_cast<const f4v*>(la + ra * ROWB + swz(ra, C0 + 2 * h + u) * 16);
+    }
+    const int col = wn * (WNT * 32) + WNT * r32;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int row = HALF * 16 + 8 * h + s;
+        f.b[s] = *reinterpret_cast<const BV*>(lb + row * (BN * 4) + col * 4);
+    }
+}
+
+template <int TM, int WNT, int I0, int I1>
+__device__ __forceinline__ void mma_step_nn(f16v (&acc)[TM][WNT], const FragsNN<TM, WNT>& f) {
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+#pragma unroll
+        for (int i = I0; i < I1; i++)
+#pragma unroll
+            for (int q = 0; q < WNT; q++)
+                acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.b[s][q], f4_at(f.a[0][i], s), acc[i][q], 0, 0, 0);
+}
+
 // Direct global -> LDS copy of one operand's K pair (two steps, 128 bytes of each row -- whole
 // L2 lines).  Each of a wave's DMA instructions fills 1 KB = 8 LDS rows; lane L lands at row
 // r = 8 p + L / 8, stored chunk L % 8, so it fetches the logical chunk that swz() stores there
@@ -235,6 +281,50 @@ __device__ __forceinline__ void dma_rows(char* lds, const S* __restrict__ base, 
     const char* kbase = reinterpret_cast<const char*>(base + k0);
 #pragma unroll
     for (int i = 0; i < N; i++) dma16(kbase + o.v[i], lds + (wave * N + i) * 1024);
+}
+
+// B slot of the N-major layout: one DMA instruction fills 1 KB = 1024 / (4 BN) K rows; wave w's
+// instruction i fills rows RPI (DMA_B w + i) ..  Columns past N load the last whole vector of the
+// row (their products land only in C columns that are never stored); N is a multiple of 4 here.
+template <int BN, int N>
+__device__ __forceinline__ DmaOffsets<N> dma_offsets_nn(uint32_t cols_valid, uint32_t ldk, int wave, int lane) {
+    constexpr int RPI = 1024 / (BN * 4);                 // rows per DMA instruction
+    constexpr int LPR = 64 / RPI;                        // lanes per row
+    DmaOffsets<N> o;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const uint32_t row = (uint32_t)((wave * N + i) * RPI + lane / LPR);
+        const uint32_t col = min((uint32_t)(lane % LPR) * 4, cols_valid - 4);
+        o.v[i] = (row * ldk + col) * 4u;
+    }
+    return o;
+}
+
+// One K step (16 rows) of the N-major B tile through registers, element loads, zero past K; rows
+// 0 .. 15 of the slot.  Thread chunk q = tid + 256 j is row q / (BN / 4), columns 4 (q % (BN / 4)).
+template <int BN> constexpr int kTailChunksNN = 16 * BN / 4 / NTHREADS;
+
+template <int BN>
+__device__ __forceinline__ void load_tile_guarded_nn(f4v (&r)[kTailChunksNN<BN>], const float* __restrict__ base,
+                                                     uint32_t cols_valid, uint32_t ldk, uint32_t k0, uint32_t K) {
+#pragma unroll
+    for (int j = 0; j < kTailChunksNN<BN>; j++) {
+        const int q = threadIdx.x + NTHREADS * j;
+        const uint32_t k = k0 + (uint32_t)(q / (BN / 4));
+        const uint32_t c = (uint32_t)(q % (BN / 4)) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            r[j][e] = (k < K && c + e < cols_valid) ? base[(uint64_t)k * ldk + c + e] : 0.0f;
+    }
+}
+
+template <int BN>
+__device__ __forceinline__ void store_tile_nn(char* lds, const f4v (&r)[kTailChunksNN<BN>]) {
+#pragma unroll
+    for (int j = 0; j < kTailChunksNN<BN>; j++) {
+        const int q = threadIdx.x + NTHREADS * j;
+        *reinterpret_cast<f4v*>(lds + (q / (BN / 4)) * (BN * 4) + (q % (BN / 4)) * 16) = r[j];
+    }
 }
 
 // s_waitcnt vmcnt(N), expcnt / lgkmcnt left at their maximum (gfx9 encoding: vmcnt in bits
@@ -317,7 +407,8 @@ __device__ __forceinline__ void ring_barrier() {
 // SPLIT: the K range is cut into g.ksplit-element pieces, one per block along the outermost
 // block-batch index; the block writes its fp32 partial tile to Cv as [split][batch][M][N]
 // (g.ldc = N, g.cn = 1), and a second kernel sums the splits in order.
-template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src>
+// BNN (fp32 only): Bt is N-major (B as [K, N]: g.ldb == 1, g.kb is B's row stride), see FragsNN.
+template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src, bool BNN = false>
 __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ Cv,
                                                              const typename MmaTraits<DT>::S* __restrict__ A,
                                                              const typename MmaTraits<DT>::S* __restrict__ Bt,
@@ -377,6 +468,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
 
+    static_assert(!BNN || DT == MX_FLOAT32, "the N-major B layout is fp32 only");
     f16v acc[TM][WNT];
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -389,16 +481,31 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     const uint32_t KP = VEC ? Klen / (2 * KSTEP) : 0;  // whole K pairs copied by LDS DMA
     // Fragments are double-buffered in registers: f0 holds a pair's first step, f1 its second;
     // each step reads the next step's fragments while its own MFMAs run.
-    Frags<DT, TM, WNT> f0, f1;
+    using FR = std::conditional_t<BNN, FragsNN<TM, WNT>, Frags<DT, TM, WNT>>;
+    FR f0, f1;
+    auto read_step = [&](auto half, FR& f, const char* la, const char* lb) {
+        constexpr int HALF = decltype(half)::value;
+        if constexpr (BNN) read_frags_nn<TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
+        else read_frags<DT, TM, WNT, HALF>(f, la, lb, wm, wn, lane);
+    };
+    auto mma = [&](auto i0, auto i1, const FR& f) {
+        constexpr int I0_ = decltype(i0)::value, I1_ = decltype(i1)::value;
+        if constexpr (BNN) mma_step_nn<TM, WNT, I0_, I1_>(acc, f);
+        else mma_step<DT, TM, WNT, I0_, I1_>(acc, f);
+    };
     const auto sa = Src::template a_init<S, DMA_A>(g, geo, m0, rows_a, wave, lane);
-    const DmaOffsets<DMA_B> ob = dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
+    const DmaOffsets<DMA_B> ob = BNN ? dma_offsets_nn<BN, DMA_B>(rows_b, g.kb, wave, lane)
+                                     : dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
     auto dma_pair = [&](auto s, uint32_t p) {
         Src::template a_dma<S, DMA_A>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
-        dma_rows<S, DMA_B>(slot_b(s), Bblk, ob, p * 2 * KSTEP, wave);
+        if constexpr (BNN) dma_rows<S, DMA_B>(slot_b(s), Bblk + (uint64_t)p * 2 * KSTEP * g.kb, ob, 0, wave);
+        else dma_rows<S, DMA_B>(slot_b(s), Bblk, ob, p * 2 * KSTEP, wave);
     };
     constexpr int H0 = TM / 2;                           // A tile rows of a step's first half
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
+    using IH = std::integral_constant<int, H0>;
+    using ITM = std::integral_constant<int, TM>;
     constexpr int PER_PAIR = DMA_A + DMA_B;              // DMA instructions per wave per pair
     // Pair p lives in slot p % 2.  Its first step reads the second step's fragments (same slot,
     // already landed) while the first step's MFMAs run; no barrier.  Its second step runs half of
@@ -415,24 +522,24 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     auto pair_steady = [&](auto s, uint32_t p) {
         using SN = std::integral_constant<int, 1 - decltype(s)::value>;
         constexpr int MF = kMfmaPerSlot<DT>;
-        read_frags<DT, TM, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
-        mma_step<DT, TM, WNT, 0, TM>(acc, f0);
+        read_step(I1{}, f1, slot_a(s), slot_b(s));
+        mma(I0{}, ITM{}, f0);
         if constexpr (DT != MX_FLOAT32) interleave_even<DT, TM, WNT>();
         __builtin_amdgcn_sched_barrier(0);
-        mma_step<DT, TM, WNT, 0, H0>(acc, f1);
+        mma(I0{}, IH{}, f1);
         if constexpr (DT != MX_FLOAT32) __builtin_amdgcn_sched_group_barrier(0x008, TM * WNT * MF, 0);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmem<0>();
         ring_barrier();
         if constexpr (DT == MX_FLOAT32) {
             // fp32: the next pair's first fragments before the DMA, so no LDS read follows it
-            read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+            read_step(I0{}, f0, slot_a(SN{}), slot_b(SN{}));
             dma_pair(s, p + 2);
         } else {
             dma_pair(s, p + 2);
-            read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+            read_step(I0{}, f0, slot_a(SN{}), slot_b(SN{}));
         }
-        mma_step<DT, TM, WNT, H0, TM>(acc, f1);
+        mma(IH{}, ITM{}, f1);
         if constexpr (DT != MX_FLOAT32) interleave_odd<DT, TM, WNT, BM, BN>();
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -440,18 +547,18 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     auto pair_drain = [&](auto s, uint32_t p) {
         using SN = std::integral_constant<int, 1 - decltype(s)::value>;
         if (p >= KP) return;
-        read_frags<DT, TM, WNT, 1>(f1, slot_a(s), slot_b(s), wm, wn, lane);
-        mma_step<DT, TM, WNT, 0, TM>(acc, f0);
-        mma_step<DT, TM, WNT, 0, H0>(acc, f1);
+        read_step(I1{}, f1, slot_a(s), slot_b(s));
+        mma(I0{}, ITM{}, f0);
+        mma(I0{}, IH{}, f1);
         // (the MFMA sequence is the same on both paths: a branch around MFMAs makes the
         // compiler shuffle the accumulators between register files)
         if (p + 1 < KP) {
             wait_vmem<0>();
             ring_barrier();
             if (p + 2 < KP) dma_pair(s, p + 2);
-            read_frags<DT, TM, WNT, 0>(f0, slot_a(SN{}), slot_b(SN{}), wm, wn, lane);
+            read_step(I0{}, f0, slot_a(SN{}), slot_b(SN{}));
         }
-        mma_step<DT, TM, WNT, H0, TM>(acc, f1);
+        mma(IH{}, ITM{}, f1);
     };
     if (KP > 0) {
         dma_pair(I0{}, 0);
@@ -462,7 +569,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
             wait_vmem<0>();
         }
         ring_barrier();
-        read_frags<DT, TM, WNT, 0>(f0, la0, lb0, wm, wn, lane);
+        read_step(I0{}, f0, la0, lb0);
         uint32_t p = 0;
         for (; p + 4 <= KP; p += 2) {                    // pairs p, p + 1 issue p + 2, p + 3
             pair_steady(I0{}, p);
@@ -479,14 +586,21 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         // first half of slot 0, zero past K.
         const S* Ablk = Abat + (uint64_t)m0 * g.lda;
         for (uint32_t kt = 2 * KP; kt < KT; kt++) {
-            uint4 ra[kTailChunks<BM>], rb[kTailChunks<BN>];
+            uint4 ra[kTailChunks<BM>];
             load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
-            load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
+            if constexpr (BNN) {
+                f4v rb[kTailChunksNN<BN>];
+                load_tile_guarded_nn<BN>(rb, reinterpret_cast<const float*>(Bblk), rows_b, g.kb, kt * KSTEP, Klen);
+                store_tile_nn<BN>(lb0, rb);
+            } else {
+                uint4 rb[kTailChunks<BN>];
+                load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
+                store_tile<BN>(lb0, rb);
+            }
             store_tile<BM>(la0, ra);
-            store_tile<BN>(lb0, rb);
             __syncthreads();
-            read_frags<DT, TM, WNT, 0>(f0, la0, lb0, wm, wn, lane);
-            mma_step<DT, TM, WNT, 0, TM>(acc, f0);
+            read_step(I0{}, f0, la0, lb0);
+            mma(I0{}, ITM{}, f0);
             __syncthreads();
         }
     }
@@ -501,6 +615,34 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         else return float_to_bf16(v);
     };
     const bool vec_store = g.cn == 1 && Src::template row_vec_ok<CT>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
+    if constexpr (BNN) {
+        // accumulator q of MFMA tile (i, .) holds, in register r, C column
+        // WNT (8 (r / 4) + 4 h + r % 4) + q of the wave's column range
+        const uint32_t cw = n0 + wn * (WNT * 32);
+        typedef float cvec __attribute__((ext_vector_type(WNT)));
+        const bool interior = m0 + BM <= g.M && n0 + BN <= g.N && vec_store;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+            if (!interior && row >= g.M) continue;
+            CT* crow = Cbat + Src::row_off(g, geo, row);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t col = cw + WNT * (8 * (r >> 2) + 4 * h + (r & 3));
+                if (interior) {
+                    cvec v;
+#pragma unroll
+                    for (int q = 0; q < WNT; q++) v[q] = acc[i][q][r];
+                    *reinterpret_cast<cvec*>(crow + col) = v;
+                } else {
+#pragma unroll
+                    for (int q = 0; q < WNT; q++)
+                        if (col + q < g.N) crow[(uint64_t)(col + q) * g.cn] = acc[i][q][r];
+                }
+            }
+        }
+        return;
+    }
     if (m0 + BM <= g.M && n0 + BN <= g.N && vec_store) {   // interior tile: 4 columns per store
 #pragma unroll
         for (int i = 0; i < TM; i++) {
@@ -551,7 +693,7 @@ inline TileShape choose_tile(uint64_t M, uint64_t N, uint64_t batches) {
 
 // Launches mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src> for the chosen shape; with SPLIT,
 // nsplit K pieces of g.ksplit elements each.
-template <int DT, bool VEC, bool SPLIT, class Src>
+template <int DT, bool VEC, bool SPLIT, class Src, bool BNN = false>
 int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C, const void* A, const void* Bt,
                        hipStream_t st, const char* who, uint32_t nsplit = 1) {
     using S = typename MmaTraits<DT>::S;
@@ -561,8 +703,8 @@ int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C
         g.tiles_n = (g.N + BN - 1) / BN;
         const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches * nsplit;
         if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": grid too large");
-        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src>), dim3((uint32_t)blocks), dim3(NTHREADS),
-                           0, st, C, (const S*)A, (const S*)Bt, g, geo);
+        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src, BNN>), dim3((uint32_t)blocks),
+                           dim3(NTHREADS), 0, st, C, (const S*)A, (const S*)Bt, g, geo);
         MX_HIP(hipGetLastError());
         return MX_OK;
     };

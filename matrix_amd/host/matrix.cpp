@@ -619,8 +619,20 @@ matrix matrix::unbroadcast_shape(const size_m* target_shape, int target_dims) co
     return result;
 }
 
+// An fp32 Bt whose N axis is unit-stride with 16-byte K rows (B contiguous as [..., K, N], seen
+// through the transpose): the GEMM reads B in that layout, so no packed copy is made.
+static bool n_major_ok(const matrix& bt) {
+    if (bt.type != dtype::Float || bt.dims < 2) return false;
+    const size_m* st = bt.strides();
+    const size_m* sh = bt.shape();
+    if (st[bt.dims - 2] != 1 || st[bt.dims - 1] % 4 || sh[bt.dims - 2] % 4 || bt.offset % 4) return false;
+    for (uint32_t d = 0; d + 2 < bt.dims; d++)
+        if (sh[d] > 1 && st[d] % 4) return false;
+    return true;
+}
+
 // dot packs B^T contiguous (and A when it is a strided view) before the product, as the
-// reference does (Matrix.mm:7068-7092).
+// reference does (Matrix.mm:7068-7092) -- except an fp32 B that is already N-major.
 matrix matrix::dot(const matrix& b, bool transposeB) const {
     if (dims < 2 || b.dims < 2) throw std::invalid_argument("matrix::dot requires both matrices to be at least 2D");
     matrix bt = b;
@@ -630,7 +642,7 @@ matrix matrix::dot(const matrix& b, bool transposeB) const {
         std::swap(axes[b.dims - 2], axes[b.dims - 1]);
         bt = b.transpose(axes);
     }
-    if (!bt.is_contiguous()) bt = bt.astype(bt.type, true);
+    if (!bt.is_contiguous() && !(type == dtype::Float && n_major_ok(bt))) bt = bt.astype(bt.type, true);
     matrix a = is_contiguous() ? *this : astype(type, true);
     if (bt.type != a.type) bt = bt.astype(a.type, true);
     uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];

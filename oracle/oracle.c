@@ -359,7 +359,9 @@ int orc_reduce(int op, int dtype, int acc_mode, uint32_t reduce_stride, uint32_t
 
 /* ---------------------------------------------------------------- batched matmul */
 /* batched_dot_cpu, Matrix.mm:7139-7196: batch offsets decomposed from the last batch axis,
- * then for (m, n): T sum = 0; for k: sum += A[idxA + k] * Bt[idxB + k]. */
+ * then for (m, n): T sum = 0; for k: sum += A[idxA + k] * Bt[idxB + k].  K is unit-stride in
+ * both operands, as dot() packs them before this loop (Matrix.mm:7068-7092): the K strides in
+ * sA / sBt are not read, so a strided operand is checked against its packed copy. */
 #define MM_LOOP(T, ACCT, STEP, OUT)                                                   \
     do {                                                                              \
         const T* pa = (const T*)A; const T* pb = (const T*)Bt; T* pc = (T*)C;         \

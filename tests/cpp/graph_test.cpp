@@ -86,6 +86,12 @@ CASE(shapes_dot_and_conv) {
     matrix c = a.dot(b);
     EXPECT(c.dims == 3 && c.shape()[0] == 16 && c.shape()[1] == 64 && c.shape()[2] == 48, "dot shape");
     EXPECT(throws([&] { (void)a.dot(matrix::leaf({31, 48})); }), "core-dimension mismatch throws");
+    // fp32 B in its [K, N] layout reaches the GEMM as the transposed view of its own storage
+    EXPECT(c.tape && c.tape->input_at(1).storage == b.storage, "fp32 N-major B is not copied");
+    matrix c16 = matrix::leaf({64, 32}, dtype::Float16).dot(matrix::leaf({32, 48}, dtype::Float16));
+    EXPECT(c16.tape->input_at(1).tape && c16.tape->input_at(1).is_contiguous(), "fp16 B^T is packed");
+    matrix c10 = a.dot(matrix::leaf({32, 10}));
+    EXPECT(c10.tape->input_at(1).is_contiguous(), "N not a multiple of 4: B^T is packed");
     matrix x = matrix::leaf({2, 56, 56, 64});
     matrix w = matrix::leaf({128, 3, 3, 64});
     matrix y = matrix::conv2d(x, w, 1, 1, 1, 1);
