@@ -144,6 +144,37 @@ def test_conv1d_mfma(mx, orc, dt):
     assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
+    # (N, H, W, C, O, kh, kw, pad_h, pad_w): more 128 x 128 output tiles than the GPU has CUs, so a
+    # block computes several tiles and fetches the next tile's K pairs while it finishes the last
+    (8, 50, 50, 64, 160, 1, 1, 0, 0),      # 1 K pair per tile, 314 tiles; O = 160: edge tiles in N
+    (5, 64, 64, 128, 144, 1, 1, 0, 0),     # 2 K pairs, 320 tiles
+    (9, 64, 64, 64, 64, 1, 3, 0, 1),       # 3 K pairs (one per tap), 288 tiles
+    (9, 64, 64, 32, 64, 3, 3, 1, 1),       # 9 K pairs (32 channels, zero-padded to the pair), 288 tiles
+])
+def test_conv2d_many_tiles(mx, orc, dt, case):
+    code = getattr(mx, dt)
+    n, h, w, c, o, kh, kw, ph, pw = case
+    rng = np.random.default_rng(n * 7919 + c * 31 + o + kw)
+    x = store_of(code, rng.standard_normal([n, h, w, c]).astype(np.float32), mx)
+    wt = store_of(code, (rng.standard_normal([o, kh, kw, c]) * np.sqrt(2.0 / (c * kh * kw))).astype(np.float32), mx)
+    got, ref = run_conv(mx, orc, code, x, [n, h, w, c], contiguous_strides([n, h, w, c]), wt, [o, kh, kw, c],
+                        contiguous_strides([o, kh, kw, c]), [ph, pw], [1, 1])
+    err = normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx))
+    assert err <= TOL[dt], (dt, case, err)
+
+
+def test_conv1d_many_tiles(mx, orc):
+    code = mx.FLOAT16
+    rng = np.random.default_rng(11)
+    x = store_of(code, rng.standard_normal([40, 1000, 64]).astype(np.float32), mx)
+    wt = store_of(code, (rng.standard_normal([72, 3, 64]) * 0.1).astype(np.float32), mx)
+    got, ref = run_conv(mx, orc, code, x, [40, 1000, 64], contiguous_strides([40, 1000, 64]), wt, [72, 3, 64],
+                        contiguous_strides([72, 3, 64]), [1], [1])
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL["FLOAT16"]
+
+
 def test_direct_fp32_is_bit_exact(mx, orc):
     """Input dilation and a 3-D conv take the direct kernel: same loop order as the CPU."""
     rng = np.random.default_rng(5)
