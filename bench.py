@@ -10,12 +10,16 @@ rows with duplicated extrema):
 inputs resident in HBM and rotated over enough copies that the 256 MB Infinity Cache cannot
 hold the working set.  The step is one execute of the workload's compiled graph through the C++
 graph API (matrix_amd/_bin/reductions_step: build once, compile once, then execute +
-clear_trace_checks per step, each execute ending in its stream wait, as execute_metal does);
-the executor runs the graph's independent reductions on two streams.
+clear_trace_checks per step, each execute ending in its stream wait, as execute_metal does).
+The executor runs independent reductions with one collapsed descriptor as one group launch
+(mx_launch_reduce_group: the five over axis 1, the five over axis 0, the five over axis 3 of the
+reshape, the three chained over axis 1 after them, ArgMax / ArgMin over axis 1 of the reshape)
+and the graph's independent parts on two streams.
 
 Prints one JSON line.  `roofline` is the dominant kernel's bytes per launch over its average
-duration (HIP events on the launch stream, one op launched back to back); `cpu_baseline` times
-the oracle (the reference's CPU loops restated) single-threaded on a bounded sample on this host.
+duration: the group launch that takes longest, timed with HIP events on its launch stream over
+back-to-back launches on rotated inputs.  `cpu_baseline` times the oracle (the reference's CPU
+loops restated) single-threaded on a bounded sample on this host.
 """
 from __future__ import annotations
 
@@ -31,7 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-N_COPIES = 6          # 6 x 64 MiB inputs > 256 MB MALL
+N_COPIES = 17         # one 64 MiB copy of X per reduction that reads it (1.1 GB > the 256 MB MALL)
 
 
 def contiguous_strides(shape):
@@ -71,6 +75,7 @@ def build_ops(mx):
 class Prepared:
     def __init__(self, mx, name, op, shape, axis, src):
         self.name, self.op, self.shape, self.axis, self.src = name, op, shape, axis, src
+        self.tag = name.split("_", 1)[1]                 # shape / axis part of the op name
         out_shape = [s for i, s in enumerate(shape) if i != axis]
         self.desc = mx.collapse_dims_reduce2(shape, contiguous_strides(out_shape), contiguous_strides(shape), axis)
         self.rs = contiguous_strides(shape)[axis]
@@ -89,6 +94,34 @@ class Prepared:
         self._launch(self.O.ptr, in_ptr)
 
 
+class PreparedGroup:
+    """The reductions of one descriptor (same shape and axis) as one mx_launch_reduce_group launch,
+    as the graph executor groups them."""
+
+    def __init__(self, mx, members):
+        self.members = members
+        m0 = members[0]
+        self.name = "group_" + m0.tag
+        self.bytes = sum(p.bytes for p in members)
+        self._launch = mx.prepare_reduce_group([p.op for p in members], mx.FLOAT32, m0.rs, m0.n, m0.desc,
+                                               [p.W.ptr if p.W else 0 for p in members], [p.ws for p in members])
+
+    def launch(self, ins):
+        self._launch([p.O.ptr for p in self.members], ins)
+
+
+def make_groups(mx, prepared):
+    """Groups of up to 8 ops with one (shape, axis), in workload order."""
+    groups, by_key = [], {}
+    for j, p in enumerate(prepared):
+        key = (tuple(p.shape), p.axis)
+        if key not in by_key or len(by_key[key][-1]) >= mx.REDUCE_GROUP_MAX:
+            by_key.setdefault(key, []).append([])
+            groups.append(by_key[key][-1])
+        by_key[key][-1].append(j)
+    return groups
+
+
 def run_gpu(args):
     import matrix_amd as mx
     mx.init(0)
@@ -96,14 +129,23 @@ def run_gpu(args):
     copies = [mx.DeviceBuffer.from_numpy(x) for _ in range(N_COPIES)]
     prepared = [Prepared(mx, *o) for o in build_ops(mx)]
     by_name = {p.name: p for p in prepared}
+    groups = [(idx, PreparedGroup(mx, [prepared[j] for j in idx])) for idx in make_groups(mx, prepared)]
+
+    # every op reading X has its own resident copy (its ordinal among the ops on X), so no read of
+    # X in a step can be served by the Infinity Cache from an earlier read of the same step
+    ordinal = {}
+    for p in prepared:
+        if p.src == "X":
+            ordinal[p.name] = len(ordinal)
+    assert len(ordinal) == N_COPIES
+
+    def src_of(p, c):
+        return copies[c % N_COPIES].ptr if p.src == "X" else by_name[p.src].O.ptr
 
     def step(i):
-        # every op reading X gets the next resident copy, so no read of X can be served by the
-        # Infinity Cache from an earlier op of the same step
-        k = i * len(prepared)
-        for j, p in enumerate(prepared):
-            src = copies[(k + j) % N_COPIES].ptr if p.src == "X" else by_name[p.src].O.ptr
-            p.launch(mx, src)
+        # the step as the executor runs it: one launch per group (members in workload order)
+        for idx, g in groups:
+            g.launch([src_of(prepared[j], ordinal.get(prepared[j].name, 0)) for j in idx])
 
     for i in range(args.warmup):
         step(i)
@@ -119,25 +161,37 @@ def run_gpu(args):
     ms_step = e0.elapsed_ms(e1) / args.steps
     step_bytes = sum(p.bytes for p in prepared)
 
-    # per-op durations (events bracket each op's launches on the same stream)
-    per_op = {}
+    # durations per group launch and per single-op launch (events bracket the launches on the
+    # launch stream): consecutive launches take the next copies, so a copy is read again only
+    # after N_COPIES - 1 other reads of X; a group's chained inputs are its producers' outputs
     reps = max(3, min(40, 2 * args.steps))
+    per_group = {}
+    for idx, g in groups:
+        a, b = mx.Event(), mx.Event()
+        a.record()
+        for i in range(reps):
+            g.launch([src_of(prepared[j], i * len(idx) + k) for k, j in enumerate(idx)])
+        b.record()
+        mx.sync()
+        per_group[g.name] = (a.elapsed_ms(b) / reps, g)
+    per_op = {}
     for p in prepared:
         a, b = mx.Event(), mx.Event()
         a.record()
         for i in range(reps):
-            src = copies[i % N_COPIES].ptr if p.src == "X" else by_name[p.src].O.ptr
-            p.launch(mx, src)
+            p.launch(mx, src_of(p, i))
         b.record()
         mx.sync()
         per_op[p.name] = a.elapsed_ms(b) / reps
-    dom = max(prepared, key=lambda p: per_op[p.name])
-    achieved = dom.bytes / (per_op[dom.name] * 1e-3) / 1e9
+    dom_name, (dom_ms, dom) = max(per_group.items(), key=lambda kv: kv[1][0])
+    achieved = dom.bytes / (dom_ms * 1e-3) / 1e9
     return {
         "ms_per_step": ms_step, "wall_s": wall, "step_bytes": step_bytes,
         "value": step_bytes / (ms_step * 1e-3) / 1e9,
-        "dominant": dom.name, "dominant_bytes": dom.bytes, "dominant_ms": per_op[dom.name],
+        "dominant": dom_name, "dominant_bytes": dom.bytes, "dominant_ms": dom_ms,
+        "dominant_members": [p.name for p in dom.members],
         "achieved": achieved,
+        "per_group_gbs": {k: round(g.bytes / (ms * 1e-3) / 1e9, 1) for k, (ms, g) in per_group.items()},
         "per_op_gbs": {k: round(by_name[k].bytes / (v * 1e-3) / 1e9, 1) for k, v in per_op.items()},
         "cpu_ops": [(p.name, p.op, p.shape, p.axis, p.src, p.desc, p.rs, p.n, p.total, p.bytes) for p in prepared],
     }
@@ -346,32 +400,47 @@ def measured_traffic(op_name):
 
 
 def kernel_probe(op_name, reps=10):
-    """For hardware-counter runs: only `op_name` of the reductions workload (reps launches on
-    rotated copies), then a 256 MiB device copy (the calibration kernel of known bytes)."""
+    """For hardware-counter runs: only `op_name` of the reductions workload -- one op, or a group
+    launch (group_axis1, group_r4_axis3, ...) -- reps launches on rotated copies, then a 256 MiB
+    device copy (the calibration kernel of known bytes)."""
     import matrix_amd as mx
     mx.init(0)
     x = make_input(0)
     copies = [mx.DeviceBuffer.from_numpy(x) for _ in range(N_COPIES)]
-    prepared = {p.name: p for p in (Prepared(mx, *o) for o in build_ops(mx))}
-    p = prepared[op_name]
-    if p.src != "X":
-        raise SystemExit(f"--kernel-probe: {op_name} reads an intermediate; pick an op on X")
-    for i in range(reps):
-        p.launch(mx, copies[i % N_COPIES].ptr)
+    prepared = [Prepared(mx, *o) for o in build_ops(mx)]
+    groups = {g.name: g for g in (PreparedGroup(mx, [prepared[j] for j in idx]) for idx in make_groups(mx, prepared))}
+    singles = {p.name: p for p in prepared}
+    if op_name in groups:
+        g = groups[op_name]
+        if any(p.src != "X" for p in g.members):
+            raise SystemExit(f"--kernel-probe: {op_name} reads intermediates; pick a group on X")
+        for i in range(reps):
+            g.launch([copies[(i * len(g.members) + k) % N_COPIES].ptr for k in range(len(g.members))])
+        nbytes = g.bytes
+    elif op_name in singles:
+        p = singles[op_name]
+        if p.src != "X":
+            raise SystemExit(f"--kernel-probe: {op_name} reads an intermediate; pick an op on X")
+        for i in range(reps):
+            p.launch(mx, copies[i % N_COPIES].ptr)
+        nbytes = p.bytes
+    else:
+        raise SystemExit(f"--kernel-probe: unknown op or group {op_name}")
     n = 64 << 20                                     # 256 MiB of float32
     src, dst = mx.DeviceBuffer(4 * n), mx.DeviceBuffer(4 * n)
     src.fill_bytes(0)
     for _ in range(reps):
         mx.launch_copy_strided(mx.FLOAT32, mx.FLOAT32, ([n], [1], [1]), dst.ptr, src.ptr)
     mx.sync()
-    print(json.dumps({"probe": op_name, "launches": reps, "bytes_per_launch": p.bytes,
+    print(json.dumps({"probe": op_name, "launches": reps, "bytes_per_launch": nbytes,
                       "calibration_copy_bytes": 2 * 4 * n}), flush=True)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--kernel-probe", default=None, metavar="OP",
-                    help="run only OP of the reductions workload and a calibration copy (for counter runs)")
+                    help="run only OP (an op or a group launch) of the reductions workload and a calibration "
+                         "copy (for counter runs)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -410,19 +479,20 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: X[256,65536] ~ N(0,1) float32, seed 0, 30% rows with duplicated maxima, "
-                f"{N_COPIES} resident copies rotated",
+                f"{N_COPIES} resident copies, one per reduction that reads X",
         "config": {"workload": "reductions X[256,65536] f32: Sum/Max/Min/ArgMax/ArgMin over axis 1 and 0, "
                                "reshape [64,4,4096,16] over axes 3 then 1",
                    "step_bytes": r["step_bytes"], "parallelism": "single GPU",
                    "executor": f"compiled graph, execute + wait per step, {g['streams']} streams"},
         "roofline": {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(r["dominant"]),
-                     "kernel": r["dominant"], "bytes_per_launch": r["dominant_bytes"],
-                     "avg_ms": round(r["dominant_ms"], 5)},
+                     "kernel": r["dominant"], "members": r["dominant_members"],
+                     "bytes_per_launch": r["dominant_bytes"], "avg_ms": round(r["dominant_ms"], 5)},
         "cpu_baseline": cpu,
         "launch_loop_one_stream": {"ms_per_step": round(r["ms_per_step"], 4), "GB/s": round(r["value"], 1),
-                                   "note": "the same ops launched back to back from Python on one stream, "
-                                           "no wait between steps"},
+                                   "note": "the step's group launches issued back to back from Python on one "
+                                           "stream, no wait between steps"},
+        "per_group_gbs": r["per_group_gbs"],
         "per_op_gbs": r["per_op_gbs"],
         "configs": configs,
     }

@@ -119,6 +119,23 @@ int mx_launch_reduce(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduc
                      void* out, const void* in, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* n (<= MX_REDUCE_GROUP_MAX) reductions of one dtype over one descriptor (the arguments of
+ * mx_launch_reduce), member k with its own op ops[k], input ins[k], output outs[k] and workspace
+ * workspaces[k] of workspace_bytes[k] bytes (its mx_reduce_workspace_bytes; the two arrays may be
+ * NULL when no member needs one).  Each output equals that of mx_launch_reduce(ops[k], ...,
+ * outs[k], ins[k], ...) bit for bit.  Float dtypes run as one launch (plus one combine launch for
+ * a split axis), the others as one launch per member.  The members must be independent: no
+ * output may overlap another output or any input.  No counterpart in the reference, which
+ * launches each Sum / Max / Min / ArgMax / ArgMin (Matrix.mm:15099-15208, Matrix.mm:14812-15059,
+ * Matrix.mm:16182-16458) on its own: the graph layer's horizontal fusion of independent
+ * reductions with the same collapsed descriptor, so that several of them stream through HBM in
+ * one launch instead of paying a launch's ramp-up and tail each. */
+#define MX_REDUCE_GROUP_MAX 8
+int mx_launch_reduce_group(int n, const int* ops, int dtype, uint32_t reduce_stride, uint32_t n_reduce,
+                           int cdims, const uint32_t* shape, const uint32_t* sOut, const uint32_t* sIn,
+                           void* const* outs, const void* const* ins, void* const* workspaces,
+                           const size_t* workspace_bytes, void* stream);
+
 /* R = A op B exactly as mx_launch_bcast_binary, and out[r] = red_op over R[r * n .. r * n + n)
  * (the values as stored in R; R must be contiguous, n must divide the result's size and
  * n * sizeof(dtype) <= 16384).  out is contiguous, one element per row (int32 for ARGMAX /

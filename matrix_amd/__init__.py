@@ -29,6 +29,7 @@ OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_HIP, ERR_NOT_INITIALIZED, ERR_WORKSPAC
 FLOAT32, FLOAT16, UINT8, INT32, INT16, UINT32, UINT16, BOOL, INT8, COMPLEX64, BFLOAT16, INT64, UINT64 = range(13)
 OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MAX, OP_MIN, OP_EQ = range(7)
 RED_SUM, RED_MAX, RED_MIN, RED_ARGMAX, RED_ARGMIN = range(5)
+REDUCE_GROUP_MAX = 8
 MAX_DIMS = 8
 
 # numpy storage dtype of every element code (16-bit floats stored as raw bits for bfloat16)
@@ -81,6 +82,8 @@ _SIGS = {
     "mx_launch_bcast_binary": ([_i, _i, _i, _u32p, _u32p, _u32p, _u32p, _vp, _vp, _vp, _vp], _i),
     "mx_reduce_workspace_bytes": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, ctypes.POINTER(_sz)], _i),
     "mx_launch_reduce": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp, _sz, _vp], _i),
+    "mx_launch_reduce_group": ([_i, _ip, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, ctypes.POINTER(_vp),
+                                ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_sz), _vp], _i),
     "mx_collapse_dims3": ([_u32p, _u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_collapse_dims2": ([_u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_collapse_dims_matmul": ([_u32p, _u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
@@ -324,6 +327,47 @@ def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=
     shape, sOut, sIn = desc
     check(lib.mx_launch_reduce(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn),
                                int(out), int(inp), int(workspace), workspace_bytes, stream))
+
+
+def _group_arrays(ops, outs, ins, workspaces, workspace_bytes):
+    n = len(ops)
+    if not (len(outs) == len(ins) == n):
+        raise ValueError("reduce group: ops, outs and ins differ in length")
+    workspaces = list(workspaces) if workspaces is not None else [0] * n
+    workspace_bytes = list(workspace_bytes) if workspace_bytes is not None else [0] * n
+    return (n, (ctypes.c_int * n)(*ops), (_vp * n)(*[int(o) for o in outs]), (_vp * n)(*[int(i) for i in ins]),
+            (_vp * n)(*[int(w) for w in workspaces]), (_sz * n)(*workspace_bytes))
+
+
+def launch_reduce_group(ops, dtype, reduce_stride, n_reduce, desc, outs, ins, workspaces=None, workspace_bytes=None,
+                        stream=None):
+    """mx_launch_reduce_group: member k reduces ins[k] with ops[k] into outs[k] (one descriptor)."""
+    shape, sOut, sIn = desc
+    n, o, po, pi, pw, pb = _group_arrays(ops, outs, ins, workspaces, workspace_bytes)
+    check(lib.mx_launch_reduce_group(n, o, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn),
+                                     po, pi, pw, pb, stream))
+
+
+def prepare_reduce_group(ops, dtype, reduce_stride, n_reduce, desc, workspaces=None, workspace_bytes=None,
+                         stream=None):
+    """mx_launch_reduce_group with its descriptor and ops converted once: returns launch(outs, ins)."""
+    shape, sOut, sIn = desc
+    n = len(ops)
+    fn = lib.mx_launch_reduce_group
+    opa = (ctypes.c_int * n)(*ops)
+    pw = (_vp * n)(*[int(w) for w in (workspaces or [0] * n)])
+    pb = (_sz * n)(*(workspace_bytes or [0] * n))
+    head = (dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn))
+    po, pi = (_vp * n)(), (_vp * n)()
+
+    def launch(outs, ins):
+        for k in range(n):
+            po[k], pi[k] = int(outs[k]), int(ins[k])
+        status = fn(n, opa, *head, po, pi, pw, pb, stream)
+        if status != OK:
+            raise MatrixAMDError(status, last_error())
+
+    return launch
 
 
 def launch_bcast_binary_reduce_rows(op, red_op, dtype, desc, n, R, A, B, out, stream=None):

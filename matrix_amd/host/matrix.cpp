@@ -711,24 +711,53 @@ void compile_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {
 }
 
 // ------------------------------------------------------------------ the executor
-// execute_gpu launches the graph's unevaluated nodes in topological order.  The pending nodes
-// split into independent parts (weakly connected components of their data dependencies: leaves
-// and nodes evaluated by an earlier execute do not connect anything); each part runs on one
-// stream, and the parts take the executor's streams round-robin (two by default;
-// MATRIX_AMD_STREAMS=1 gives the reference's single in-order queue).  Independent reductions of
-// one input thus overlap -- one kernel's tail with another's start -- while a connected graph
-// such as a training step stays on one stream and needs no cross-stream waits.  Every stream
-// then joins the calling thread's stream, which execute waits on once, as execute_metal commits
-// and waits (Matrix.mm:8452-8475).
+// execute_gpu launches the graph's unevaluated nodes in topological order.
+// * Horizontal fusion: pending reductions of one float dtype over one collapsed descriptor that
+//   do not depend on each other run as one mx_launch_reduce_group launch (a unit; up to 8
+//   members), so several of them stream through HBM in one launch instead of paying a launch's
+//   ramp-up and tail each (MATRIX_AMD_GROUP=0 launches every node on its own).  A reduction fused
+//   into its broadcast producer is never grouped.  Units run in a topological order of units.
+// * Streams: the pending nodes split into independent parts (weakly connected components of their
+//   data dependencies, a group's members joined into one part: leaves and nodes evaluated by an
+//   earlier execute do not connect anything); each part runs on one stream, and the parts take
+//   the executor's streams round-robin (two by default; MATRIX_AMD_STREAMS=1 gives the
+//   reference's single in-order queue).  Independent work thus overlaps -- one kernel's tail with
+//   another's start -- while a connected graph such as a training step stays on one stream and
+//   needs no cross-stream waits.
+// Every stream then joins the calling thread's stream, which execute waits on once, as
+// execute_metal commits and waits (Matrix.mm:8452-8475).
+// What an execute launches: the pending nodes in `order` (a group's members together), node i on
+// the executor's stream stream_of[i].  Computed on the first execute of a set of outputs and
+// replayed while it holds -- the same outputs, every scheduled node pending again, every boundary
+// node still evaluated (execute + clear_trace_checks, as a compiled graph runs) -- so a repeated
+// execute spends no host time on walking, grouping and ordering the graph.
+struct Schedule {
+    std::vector<const Primitive*> roots;
+    std::vector<matrix> nodes, leaves;
+    std::vector<const Primitive*> boundary;
+    std::vector<int> order;                              // node indices, a group's members together
+    std::vector<int> group_of, stream_of;
+    std::vector<std::vector<int>> groups;
+    std::vector<bool> used;
+};
+
 struct Executor {
     std::vector<void*> streams;     // [0] is the thread's stream
     std::vector<void*> events;
     int count = 0;
+    bool group = true;
+    // the schedules of the last few output sets, most recent first; they hold their graphs.  Like
+    // the streams, never destroyed: a thread-exit destructor freeing device memory could run
+    // after the HIP runtime has shut down.
+    static constexpr size_t kSchedules = 4;
+    std::vector<Schedule>& schedules = *new std::vector<Schedule>();
     Executor() {
         const char* env = std::getenv("MATRIX_AMD_STREAMS");
         count = env ? std::atoi(env) : 2;
         if (count < 1) count = 1;
         if (count > 8) count = 8;
+        const char* genv = std::getenv("MATRIX_AMD_GROUP");
+        group = !genv || std::atoi(genv) != 0;
     }
     // The streams and events live until the process ends: releasing them from a thread-exit
     // destructor could run after the HIP runtime has shut down.
@@ -760,16 +789,29 @@ Executor& executor() {
     return ex;
 }
 
-void collect(const matrix& m, std::vector<matrix>& nodes, std::unordered_map<const Primitive*, int>& index) {
+// The pending nodes reachable from the outputs (inputs first), the leaves reached (uploaded at
+// run time when written on the host) and the evaluated nodes the walk stopped at (the schedule's
+// boundary).
+struct Walk {
+    std::vector<matrix> nodes, leaves;
+    std::vector<const Primitive*> boundary;
+    std::unordered_map<const Primitive*, int> index;
+};
+
+void collect(const matrix& m, Walk& w) {
     if (!m.tape) {
-        if (m.storage->dev_stale) m.storage->upload();      // leaf written on the host
+        w.leaves.push_back(m);
         return;
     }
-    if (m.tape->evaluated || index.count(m.tape.get())) return;
+    if (w.index.count(m.tape.get())) return;
+    if (m.tape->evaluated) {
+        w.boundary.push_back(m.tape.get());
+        return;
+    }
     if (!m.tape->compiled) throw std::logic_error("matrix: execute before compile");
-    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) collect(m.tape->input_at(i), nodes, index);
-    index[m.tape.get()] = (int)nodes.size();
-    nodes.push_back(m);
+    for (uint32_t i = 0; i < m.tape->num_inputs(); i++) collect(m.tape->input_at(i), w);
+    w.index[m.tape.get()] = (int)w.nodes.size();
+    w.nodes.push_back(m);
 }
 
 int find_root(std::vector<int>& parent, int i) {
@@ -777,50 +819,242 @@ int find_root(std::vector<int>& parent, int i) {
     return i;
 }
 
-void run_graph(std::vector<matrix>& ms) {
-    std::vector<matrix> nodes;
-    std::unordered_map<const Primitive*, int> index;
-    for (auto& m : ms) collect(m, nodes, index);
-    std::vector<int> parent(nodes.size());
-    std::iota(parent.begin(), parent.end(), 0);
-    for (size_t i = 0; i < nodes.size(); i++) {         // parts: union with every pending input
+// A reduction node that may join a group launch, and its group key (dtype and descriptor).
+ReducePrim* groupable(Primitive* p) {
+    auto* r = dynamic_cast<ReducePrim*>(p);
+    if (!r || r->producer) return nullptr;
+    const int t = (int)r->in.type;
+    return (t == MX_FLOAT32 || t == MX_FLOAT16 || t == MX_BFLOAT16) ? r : nullptr;
+}
+
+std::vector<uint32_t> group_key(const ReducePrim* r) {
+    std::vector<uint32_t> k = {(uint32_t)r->in.type, r->rstride, r->n, r->cd};
+    for (uint32_t i = 0; i < r->cd; i++) { k.push_back(r->cs[i]); k.push_back(r->sOut[i]); k.push_back(r->sIn[i]); }
+    return k;
+}
+
+struct KeyHash {
+    size_t operator()(const std::vector<uint32_t>& k) const {
+        size_t h = 1469598103934665603ull;
+        for (uint32_t v : k) h = (h ^ v) * 1099511628211ull;
+        return h;
+    }
+};
+
+void launch_group(const std::vector<int>& members, const std::vector<matrix>& nodes, void* stream) {
+    int ops[MX_REDUCE_GROUP_MAX];
+    void* outs[MX_REDUCE_GROUP_MAX];
+    const void* ins[MX_REDUCE_GROUP_MAX];
+    void* ws[MX_REDUCE_GROUP_MAX];
+    size_t wsb[MX_REDUCE_GROUP_MAX];
+    const int n = (int)members.size();
+    auto* r0 = static_cast<ReducePrim*>(nodes[members[0]].tape.get());
+    for (int k = 0; k < n; k++) {
+        auto* r = static_cast<ReducePrim*>(nodes[members[k]].tape.get());
+        ops[k] = r->op;
+        outs[k] = dptr(nodes[members[k]]);
+        ins[k] = dptr(r->in);
+        ws[k] = r->ws.p;
+        wsb[k] = r->ws.bytes;
+    }
+    check(mx_launch_reduce_group(n, ops, (int)r0->in.type, r0->rstride, r0->n, (int)r0->cd, r0->cs, r0->sOut, r0->sIn,
+                                 outs, ins, ws, wsb, stream),
+          "launch reduction group");
+}
+
+Schedule build_schedule(std::vector<matrix>& ms, Executor& ex) {
+    Walk w;
+    for (auto& m : ms) collect(m, w);
+    Schedule sc;
+    for (auto& m : ms) sc.roots.push_back(m.tape.get());
+    std::vector<matrix>& nodes = w.nodes;
+    std::unordered_map<const Primitive*, int>& index = w.index;
+    const int N = (int)nodes.size();
+    std::vector<std::vector<int>> deps(N);               // pending inputs of each node
+    for (int i = 0; i < N; i++) {
         Primitive* p = nodes[i].tape.get();
         for (uint32_t j = 0; j < p->num_inputs(); j++) {
             const matrix& in = p->input_at(j);
             if (!in.tape) continue;
             auto it = index.find(in.tape.get());
-            if (it == index.end()) continue;
-            const int a = find_root(parent, (int)i), b = find_root(parent, it->second);
-            if (a != b) parent[std::max(a, b)] = std::min(a, b);
+            if (it != index.end()) deps[i].push_back(it->second);
         }
     }
-    Executor& ex = executor();
+
+    // groups: greedy in topological order; a node joins an open group of its key when none of the
+    // group's members is among its (transitive) pending ancestors
+    std::vector<int> group_of(N, -1);
+    std::vector<std::vector<int>> groups;
+    if (ex.group) {
+        std::vector<int> eidx(N, -1);                    // index among groupable nodes
+        int E = 0;
+        for (int i = 0; i < N; i++)
+            if (groupable(nodes[i].tape.get())) eidx[i] = E++;
+        if (E > 1) {
+            const int W = (E + 63) / 64;
+            std::vector<uint64_t> anc((size_t)N * W, 0);     // groupable ancestors, bitsets
+            for (int i = 0; i < N; i++)
+                for (int j : deps[i]) {
+                    for (int w = 0; w < W; w++) anc[(size_t)i * W + w] |= anc[(size_t)j * W + w];
+                    if (eidx[j] >= 0) anc[(size_t)i * W + eidx[j] / 64] |= 1ull << (eidx[j] % 64);
+                }
+            std::unordered_map<std::vector<uint32_t>, std::vector<int>, KeyHash> open;   // key -> group ids
+            for (int i = 0; i < N; i++) {
+                if (eidx[i] < 0) continue;
+                auto& cand = open[group_key(static_cast<ReducePrim*>(nodes[i].tape.get()))];
+                int gid = -1;
+                for (int g : cand) {
+                    if ((int)groups[g].size() >= MX_REDUCE_GROUP_MAX) continue;
+                    bool dep = false;
+                    for (int m : groups[g])
+                        if (anc[(size_t)i * W + eidx[m] / 64] >> (eidx[m] % 64) & 1) { dep = true; break; }
+                    if (!dep) { gid = g; break; }
+                }
+                if (gid < 0) {
+                    gid = (int)groups.size();
+                    groups.emplace_back();
+                    cand.push_back(gid);
+                }
+                groups[gid].push_back(i);
+                group_of[i] = gid;
+            }
+            for (size_t g = 0; g < groups.size(); g++)       // a group of one is a plain node
+                if (groups[g].size() == 1) { group_of[groups[g][0]] = -1; groups[g].clear(); }
+        }
+    }
+
+    // units: a group, or a node outside every group; run in a topological order of units (Kahn,
+    // earliest first member first).  Should grouping ever close a cycle between two groups, every
+    // node runs on its own in the original order.
+    std::vector<int> order;                              // node indices, a group's members together
+    {
+        const int G = (int)groups.size();
+        auto unit_of = [&](int i) { return group_of[i] >= 0 ? group_of[i] : G + i; };
+        const int U = G + N;
+        std::vector<int> indeg(U, 0), first(U, N);
+        std::vector<std::vector<int>> succ(U);
+        std::vector<bool> live(U, false);
+        for (int i = 0; i < N; i++) {
+            const int u = unit_of(i);
+            live[u] = true;
+            first[u] = std::min(first[u], i);
+            for (int j : deps[i]) {
+                const int v = unit_of(j);
+                if (v != u) { succ[v].push_back(u); indeg[u]++; }
+            }
+        }
+        std::vector<std::pair<int, int>> heap;           // (first member, unit), min-heap
+        auto cmp = [](const std::pair<int, int>& a, const std::pair<int, int>& b) { return a > b; };
+        for (int u = 0; u < U; u++)
+            if (live[u] && indeg[u] == 0) heap.push_back({first[u], u});
+        std::make_heap(heap.begin(), heap.end(), cmp);
+        while (!heap.empty()) {
+            std::pop_heap(heap.begin(), heap.end(), cmp);
+            const int u = heap.back().second;
+            heap.pop_back();
+            if (u < G) for (int m : groups[u]) order.push_back(m);
+            else order.push_back(u - G);
+            for (int v : succ[u])
+                if (--indeg[v] == 0) { heap.push_back({first[v], v}); std::push_heap(heap.begin(), heap.end(), cmp); }
+        }
+        if ((int)order.size() != N) {
+            order.resize(N);
+            std::iota(order.begin(), order.end(), 0);
+            std::fill(group_of.begin(), group_of.end(), -1);
+            groups.clear();
+        }
+    }
+
+    // parts: union with every pending input, and a group's members with each other
+    std::vector<int> parent(N);
+    std::iota(parent.begin(), parent.end(), 0);
+    auto unite = [&](int a, int b) {
+        a = find_root(parent, a);
+        b = find_root(parent, b);
+        if (a != b) parent[std::max(a, b)] = std::min(a, b);
+    };
+    for (int i = 0; i < N; i++)
+        for (int j : deps[i]) unite(i, j);
+    for (auto& g : groups)
+        for (size_t k = 1; k < g.size(); k++) unite(g[0], g[k]);
+
     const int K = ex.count;
     std::unordered_map<int, int> part_stream;
-    std::vector<bool> used(K, false);
-    used[0] = true;
-    for (size_t i = 0; i < nodes.size(); i++) {
+    sc.used.assign(K, false);
+    sc.used[0] = true;
+    sc.stream_of.assign(N, 0);
+    for (int i : order) {
+        if (nodes[i].tape->is_view()) continue;
+        const int root = find_root(parent, i);
+        auto it = part_stream.find(root);
+        const int k = it != part_stream.end() ? it->second : (int)(part_stream.size() % K);
+        if (it == part_stream.end()) part_stream.emplace(root, k);
+        sc.used[k] = true;
+        sc.stream_of[i] = k;
+    }
+    sc.order = std::move(order);
+    sc.group_of = std::move(group_of);
+    sc.groups = std::move(groups);
+    sc.nodes = std::move(w.nodes);
+    sc.leaves = std::move(w.leaves);
+    sc.boundary = std::move(w.boundary);
+    return sc;
+}
+
+bool schedule_holds(const Schedule& sc, const std::vector<matrix>& ms) {
+    if (sc.roots.size() != ms.size()) return false;
+    for (size_t i = 0; i < ms.size(); i++)
+        if (sc.roots[i] != ms[i].tape.get()) return false;
+    for (const matrix& n : sc.nodes)
+        if (n.tape->evaluated) return false;
+    for (const Primitive* b : sc.boundary)
+        if (!b->evaluated) return false;
+    return true;
+}
+
+void run_schedule(const Schedule& sc, Executor& ex) {
+    for (const matrix& l : sc.leaves)
+        if (l.storage->dev_stale) l.storage->upload();      // leaf written on the host
+    const auto& nodes = sc.nodes;
+    for (size_t oi = 0; oi < sc.order.size(); oi++) {
+        const int i = sc.order[oi];
         Primitive* p = nodes[i].tape.get();
         if (!p->is_view()) {
-            const int root = find_root(parent, (int)i);
-            auto it = part_stream.find(root);
-            const int k = it != part_stream.end() ? it->second : (int)(part_stream.size() % K);
-            if (it == part_stream.end()) part_stream.emplace(root, k);
-            used[k] = true;
-            p->stream = ex.stream(k);
+            p->stream = ex.stream(sc.stream_of[i]);
+            if (sc.group_of[i] >= 0) {                   // the whole group, then skip its members
+                const auto& g = sc.groups[sc.group_of[i]];
+                launch_group(g, nodes, p->stream);
+                for (int m : g) nodes[m].tape->evaluated = true;
+                oi += g.size() - 1;
+                continue;
+            }
             p->execute(nodes[i]);
         }
         p->evaluated = true;
     }
     void* s0 = ex.stream(0);
     int nev = 0;
-    for (int k = 1; k < K; k++) {                        // join into the thread's stream
-        if (!used[k]) continue;
+    for (int k = 1; k < (int)sc.used.size(); k++) {      // join into the thread's stream
+        if (!sc.used[k]) continue;
         void* e = ex.event(nev++);
         check(mx_hip_event_record(e, ex.stream(k)), "event record");
         check(mx_hip_stream_wait_event(s0, e), "stream wait");
     }
     check(mx_hip_sync(s0), "execute");
+}
+
+void run_graph(std::vector<matrix>& ms) {
+    Executor& ex = executor();
+    for (size_t c = 0; c < ex.schedules.size(); c++)
+        if (schedule_holds(ex.schedules[c], ms)) {
+            if (c) std::swap(ex.schedules[c], ex.schedules[0]);      // most recent first
+            run_schedule(ex.schedules[0], ex);
+            return;
+        }
+    Schedule sc = build_schedule(ms, ex);
+    run_schedule(sc, ex);
+    ex.schedules.insert(ex.schedules.begin(), std::move(sc));
+    if (ex.schedules.size() > Executor::kSchedules) ex.schedules.pop_back();
 }
 
 void clear_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {

@@ -1,11 +1,14 @@
 // reductions_step.cpp -- the reductions workload as a compiled graph through the C++ graph API.
 //
 // X[256, 65536] float32 ~ N(0,1) (seed 0; in 30% of the rows the row maximum is copied to 1-3
-// more positions, and the minimum likewise, to exercise first-index ties), held in 6 resident
-// copies so that consecutive reductions never read data the 256 MB Infinity Cache still holds.
+// more positions, and the minimum likewise, to exercise first-index ties), held in 17 resident
+// copies, one per reduction that reads X, so that no read of X in a step can be served by the
+// 256 MB Infinity Cache from an earlier read of the same step (the executor runs independent
+// reductions together, as group launches on two streams).
 // The graph: Sum / Max / Min / ArgMax / ArgMin over axis 1 and over axis 0 of X; on
 // X.reshape(64, 4, 4096, 16): Sum / Max / Min over axis 3 then axis 1, ArgMax / ArgMin over axis 3
-// and over axis 1.  Reduction j reads copy j % 6.  Built and compiled once, then executed `steps`
+// and over axis 1.  The j-th reduction that reads X reads copy j.  Built and compiled once, then
+// executed `steps`
 // times (execute + clear_trace_checks), as compile_metal / execute_metal do (Matrix.mm:8452-8475).
 //
 //   reductions_step [--steps K] [--warmup W]
@@ -43,11 +46,11 @@ int main(int argc, char** argv) {
             for (int t = 0; t < k; t++) row[(size_t)(u(g) * Cc) % Cc] = mn;
         }
         std::vector<matrix> X;
-        for (int c = 0; c < 6; c++) X.push_back(matrix::from_host<float>({R, Cc}, xv));
+        for (int c = 0; c < 17; c++) X.push_back(matrix::from_host<float>({R, Cc}, xv));
         std::vector<matrix> outs;
         double bytes = 0;
         int j = 0;
-        auto x = [&]() -> matrix& { return X[(j++) % 6]; };
+        auto x = [&]() -> matrix& { return X[(j++) % X.size()]; };
         const double xb = (double)R * Cc * 4;
         for (int axis : {1, 0}) {
             const double ob = (axis == 1 ? R : Cc) * 4.0;

@@ -213,6 +213,96 @@ CASE(gpu_fused_reduction_lifecycle) {
     }
 }
 
+// Independent reductions with one descriptor run as group launches (horizontal fusion): five over
+// axis 1, three over axis 0, two over axis 3 of a reshape and the two chained over axis 1 after
+// them.  d reduces with the axis-0 descriptor but depends on one of that group's members, so it
+// must run after the group, not in it.  Every output equals host loops, also when executed again
+// after a leaf changes.
+CASE(gpu_grouped_reductions) {
+    const size_m R = 96, Cc = 4096;
+    std::vector<std::vector<float>> xv;
+    std::vector<matrix> x;
+    for (int k = 0; k < 4; k++) {
+        auto v = randn((size_t)R * Cc, 40 + k);
+        for (size_t r = 0; r < R; r += 3) v[r * Cc + 7] = v[r * Cc + 900] = 5.0f;   // ties of the row maxima
+        xv.push_back(v);
+        x.push_back(matrix::from_host<float>({R, Cc}, v));
+    }
+    const std::vector<size_m> r4 = {R, 4, 64, 16};
+    matrix a_max0 = x[1].max(0);
+    matrix d = (x[0] + a_max0.unsqueeze(0)).max(0);
+    std::vector<matrix> outs{x[0].sum(1), x[1].max(1), x[2].min(1), x[3].argmax(1), x[0].argmin(1),
+                             x[1].sum(0), a_max0, x[3].argmin(0), d,
+                             x[2].reshape(r4).sum(3).sum(1), x[3].reshape(r4).max(3).max(1)};
+    auto check = [&](const char* when) {
+        auto at = [&](int k, size_t r, size_t c) { return xv[k][r * Cc + c]; };
+        // axis 1
+        auto s1 = outs[0].to_host<float>(); auto m1 = outs[1].to_host<float>(); auto n1 = outs[2].to_host<float>();
+        auto am1 = outs[3].to_host<int32_t>(); auto an1 = outs[4].to_host<int32_t>();
+        for (size_t r = 0; r < R; r++) {
+            double s = 0, mag = 0;
+            float mx = -3.4028234663852886e38f, mn = 3.4028234663852886e38f, amv = mx, anv = mn;
+            int32_t ia = 0, in_ = 0;
+            for (size_t c = 0; c < Cc; c++) {
+                s += at(0, r, c); mag += std::fabs(at(0, r, c));
+                if (mx < at(1, r, c)) mx = at(1, r, c);
+                if (at(2, r, c) < mn) mn = at(2, r, c);
+                if (at(3, r, c) > amv) { amv = at(3, r, c); ia = (int32_t)c; }
+                if (at(0, r, c) < anv) { anv = at(0, r, c); in_ = (int32_t)c; }
+            }
+            EXPECT(std::fabs(s1[r] - s) <= 1e-4 * mag, std::string("axis-1 sum ") + when);
+            EXPECT(m1[r] == mx && n1[r] == mn, std::string("axis-1 max / min ") + when);
+            EXPECT(am1[r] == ia && an1[r] == in_, std::string("axis-1 argmax / argmin ") + when);
+        }
+        // axis 0, and d = max over rows of x0 + max0(x1)
+        auto s0 = outs[5].to_host<float>(); auto m0 = outs[6].to_host<float>();
+        auto an0 = outs[7].to_host<int32_t>(); auto dg = outs[8].to_host<float>();
+        for (size_t c = 0; c < Cc; c++) {
+            double s = 0, mag = 0;
+            float mx = -3.4028234663852886e38f, anv = 3.4028234663852886e38f;
+            int32_t in_ = 0;
+            for (size_t r = 0; r < R; r++) {
+                s += at(1, r, c); mag += std::fabs(at(1, r, c));
+                if (mx < at(1, r, c)) mx = at(1, r, c);
+                if (at(3, r, c) < anv) { anv = at(3, r, c); in_ = (int32_t)r; }
+            }
+            float dm = -3.4028234663852886e38f;
+            for (size_t r = 0; r < R; r++) { const float v = at(0, r, c) + mx; if (dm < v) dm = v; }
+            EXPECT(std::fabs(s0[c] - s) <= 1e-4 * mag, std::string("axis-0 sum ") + when);
+            EXPECT(m0[c] == mx && an0[c] == in_, std::string("axis-0 max / argmin ") + when);
+            EXPECT(dg[c] == dm, std::string("dependent reduction ") + when);
+        }
+        // chains over the reshape [R, 4, 64, 16]: axis 3, then axis 1
+        auto cs = outs[9].to_host<float>(); auto cm = outs[10].to_host<float>();
+        for (size_t r = 0; r < R; r++)
+            for (size_t j = 0; j < 64; j++) {
+                double s = 0, mag = 0;
+                float mx = -3.4028234663852886e38f;
+                for (size_t q = 0; q < 4; q++) {
+                    float m3 = -3.4028234663852886e38f;
+                    for (size_t t = 0; t < 16; t++) {
+                        const size_t c = q * 1024 + j * 16 + t;
+                        s += at(2, r, c); mag += std::fabs(at(2, r, c));
+                        if (m3 < at(3, r, c)) m3 = at(3, r, c);
+                    }
+                    if (mx < m3) mx = m3;
+                }
+                EXPECT(std::fabs(cs[r * 64 + j] - s) <= 1e-4 * mag, std::string("chained sum ") + when);
+                EXPECT(cm[r * 64 + j] == mx, std::string("chained max ") + when);
+            }
+    };
+    matrix::compile_gpu(outs);
+    matrix::execute_gpu(outs);
+    check("first run");
+    auto v2 = randn((size_t)R * Cc, 50);
+    std::memcpy(x[3].host_data(), v2.data(), v2.size() * sizeof(float));
+    xv[3] = v2;
+    x[3].mark_changed();
+    matrix::clear_trace_checks(outs);
+    matrix::execute_gpu(outs);
+    check("after mark_changed");
+}
+
 CASE(gpu_reductions_and_views) {
     const size_m R = 64, Cc = 4 * 256 * 16;
     auto xv = randn((size_t)R * Cc, 2);
@@ -439,6 +529,7 @@ int main(int argc, char** argv) {
     } else {
         run("gpu_add_then_rowsum", gpu_add_then_rowsum);
         run("gpu_fused_reduction_lifecycle", gpu_fused_reduction_lifecycle);
+        run("gpu_grouped_reductions", gpu_grouped_reductions);
         run("gpu_reductions_and_views", gpu_reductions_and_views);
         run("gpu_dot_batched_broadcast", gpu_dot_batched_broadcast);
         run("gpu_conv2d_nchw_views", gpu_conv2d_nchw_views);

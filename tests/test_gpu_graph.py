@@ -1,5 +1,6 @@
 """The C++ graph layer on the GPU (tests/cpp/graph_test.cpp, mode `gpu`): broadcast add then
-row-sum, the fused broadcast + reduction across re-executions, reductions over views, batched dot, conv2d on NCHW views, a compiled MLP training step
+row-sum, the fused broadcast + reduction across re-executions, reductions run as group launches,
+reductions over views, batched dot, conv2d on NCHW views, a compiled MLP training step
 (forward loss and every parameter gradient, executed three times with new inputs) and
 value_and_grad, each against double-precision host loops of the same mathematics."""
 import subprocess
@@ -17,4 +18,4 @@ def test_graph_on_gpu():
     out = subprocess.run([str(BIN), "gpu"], capture_output=True, text=True, timeout=110)
     print(out.stdout)
     assert out.returncode == 0, out.stdout + out.stderr
-    assert "FAIL" not in out.stdout and out.stdout.count("PASS") == 7, out.stdout
+    assert "FAIL" not in out.stdout and out.stdout.count("PASS") == 8, out.stdout
