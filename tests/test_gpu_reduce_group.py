@@ -19,7 +19,10 @@ pytestmark = pytest.mark.gpu
 ALL_OPS = ["RED_SUM", "RED_MAX", "RED_MIN", "RED_ARGMAX", "RED_ARGMIN"]
 
 PLAN_CASES = [
-    ([4096, 16], 1),          # lane: rows of 4 vectors
+    ([4096, 16], 1),          # lane: rows of 4 vectors (f32)
+    ([1000, 16], 1),          # lane with a partial last block
+    ([777, 32], 1),           # lane for 16-bit types (4 vectors), rows for 32-bit
+    ([500, 12], 1),           # lane: 3 vectors
     ([1000, 200], 1),         # rows: 50 vectors per row
     ([256, 32768], 1),        # block, 16 waves, one block per output
     ([16, 65536], 1),         # block, axis split over blocks (16 outputs), combine launch
