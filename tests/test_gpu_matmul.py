@@ -203,16 +203,17 @@ def test_skinny_path(mx, orc, dt, case):
         assert normwise_rel(got, ref64.reshape(-1)) <= 1e-5
 
 
-def test_skinny_one_hot_exact(mx, orc):
-    """One-hot A rows pick Bt columns exactly: C[m, n] = Bt[n, k_m]."""
-    rng = np.random.default_rng(15)
+@pytest.mark.parametrize("M", [16, 8, 3])
+def test_skinny_one_hot_exact(mx, orc, M):
+    """One-hot A rows pick Bt columns exactly: C[m, n] = Bt[n, k_m], for 16, 8 and 3 rows of A."""
+    rng = np.random.default_rng(15 + M)
     K, N = 512, 4096
-    ks = rng.integers(0, K, 16)
-    a = np.zeros([16, K], np.float32)
-    a[np.arange(16), ks] = 1.0
+    ks = rng.integers(0, K, M)
+    a = np.zeros([M, K], np.float32)
+    a[np.arange(M), ks] = 1.0
     bt = rng.standard_normal([N, K]).astype(np.float32)
     got, _, _ = run_mm(mx, orc, mx.FLOAT32, a, bt)
-    assert np.array_equal(got.reshape(16, N), bt[:, ks].T)
+    assert np.array_equal(got.reshape(M, N), bt[:, ks].T)
 
 
 @pytest.mark.parametrize("case", [
