@@ -343,15 +343,17 @@ __device__ __forceinline__ void wait_vmem() {
 // latency is several MFMAs) before the next step's first MFMA needs them.
 template <int DT> constexpr int kMfmaPerSlot = DT == MX_FLOAT32 ? 4 : 1;
 
-// First step of a pair: the next step's fragment reads, one per leading MFMA slot.
+// First step of a pair: the next step's fragment reads, one after each leading MFMA slot.  The
+// pair's first MFMA goes before the first read: LDS reads complete in order, so an MFMA behind a
+// new read would wait for that read as well as for its own (long since loaded) fragments.
 template <int DT, int TM, int WNT>
 __device__ __forceinline__ void interleave_even() {
     constexpr int MF = kMfmaPerSlot<DT>, SLOTS = 2 * TM * WNT, NR = 2 * (TM + WNT);
     static_assert(NR <= SLOTS, "interleave counts");
 #pragma unroll
     for (int i = 0; i < NR; i++) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     if constexpr (SLOTS > NR) __builtin_amdgcn_sched_group_barrier(0x008, (SLOTS - NR) * MF, 0);
 }
