@@ -20,6 +20,14 @@ __global__ __launch_bounds__(256) void reduce_lane_kernel(OutOf<DT, OP>* __restr
     lane_body<DT, OP, VEC, NV>(out, in, total_out, nv, od, blockIdx.x);
 }
 
+template <int DT, int OP, int VEC>
+__global__ __launch_bounds__(256) void reduce_lane_packed_kernel(OutOf<DT, OP>* __restrict__ out,
+                                                                 const ElemOf<DT>* __restrict__ in, uint32_t total_out,
+                                                                 uint32_t nv) {
+    __shared__ VecT<ElemOf<DT>, VEC> sh[1024];
+    lane_packed_body<DT, OP, VEC>(out, in, total_out, nv, blockIdx.x, sh);
+}
+
 template <int DT, int OP, int VEC, int WAVES, int U>
 __global__ __launch_bounds__(64 * WAVES) void reduce_block_kernel(OutOf<DT, OP>* __restrict__ out,
                                                                   StOf<DT, OP>* __restrict__ part,
@@ -86,7 +94,8 @@ int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, h
     const bool vec = p.vec == VEC && VEC > 1;
     if (p.mode == kLane) {
         dim3 grid(p.blocks);
-        if (vec) hipLaunchKernelGGL((reduce_lane_kernel<DT, OP, VEC, 4>), grid, dim3(256), 0, st, out, in, p.total_out, p.nv, od);
+        if (p.packed) hipLaunchKernelGGL((reduce_lane_packed_kernel<DT, OP, VEC>), grid, dim3(256), 0, st, out, in, p.total_out, p.nv);
+        else if (vec) hipLaunchKernelGGL((reduce_lane_kernel<DT, OP, VEC, 4>), grid, dim3(256), 0, st, out, in, p.total_out, p.nv, od);
         else hipLaunchKernelGGL((reduce_lane_kernel<DT, OP, 1, 4>), grid, dim3(256), 0, st, out, in, p.total_out, p.nv, od);
     } else if (p.mode == kShort) {
         const uint32_t gx = (uint32_t)((p.total_out + 64ull * p.waves * p.vec - 1) / (64ull * p.waves * p.vec));

@@ -37,6 +37,16 @@ __global__ __launch_bounds__(256) void reduce_lane_group_kernel(GroupPtrs gp, ui
     });
 }
 
+template <int DT, int VEC>
+__global__ __launch_bounds__(256) void reduce_lane_packed_group_kernel(GroupPtrs gp, uint32_t total_out, uint32_t nv) {
+    __shared__ VecT<ElemOf<DT>, VEC> sh[1024];
+    const int k = blockIdx.z;
+    op_switch(gp.op[k], [&](auto o) {
+        MX_GROUP_MEMBER(o);
+        lane_packed_body<DT, OP, VEC>(out, in, total_out, nv, blockIdx.x, sh);
+    });
+}
+
 template <int DT, int VEC, int WAVES, int U>
 __global__ __launch_bounds__(64 * WAVES) void reduce_block_group_kernel(GroupPtrs gp, uint32_t total_out, uint32_t n,
                                                                         uint32_t chunk, uint32_t nsplit, OffDesc od) {
@@ -132,7 +142,8 @@ int run_reduce_group(const Desc& d, int n, const int* ops, void* const* outs, co
     const uint32_t nz = (uint32_t)n;
     if (p.mode == kLane) {
         const dim3 grid(p.blocks, 1, nz);
-        if (vec) hipLaunchKernelGGL((reduce_lane_group_kernel<DT, VEC, 4>), grid, dim3(256), 0, st, gp, p.total_out, p.nv, od);
+        if (p.packed) hipLaunchKernelGGL((reduce_lane_packed_group_kernel<DT, VEC>), grid, dim3(256), 0, st, gp, p.total_out, p.nv);
+        else if (vec) hipLaunchKernelGGL((reduce_lane_group_kernel<DT, VEC, 4>), grid, dim3(256), 0, st, gp, p.total_out, p.nv, od);
         else hipLaunchKernelGGL((reduce_lane_group_kernel<DT, 1, 4>), grid, dim3(256), 0, st, gp, p.total_out, p.nv, od);
     } else if (p.mode == kShort) {
         const uint32_t gx = (uint32_t)((p.total_out + 64ull * p.waves * p.vec - 1) / (64ull * p.waves * p.vec));

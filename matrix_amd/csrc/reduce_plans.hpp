@@ -65,6 +65,26 @@ struct OffDesc {
 template <typename S, int VEC>
 struct alignas(VEC * sizeof(S) >= 16 ? 16 : VEC * sizeof(S)) VecT { S v[VEC]; };
 
+// Streaming loads of the reduced input (read exactly once), for plans whose load instructions
+// each cover whole 128-byte lines: nontemporal loads raise the axis-1 and axis-0 reductions of a
+// [256, 65536] f32 input from 5.80 to 6.24 TB/s and from 5.74 to 6.40 TB/s.  The lane plan keeps
+// ordinary loads: each lane's row is split over several load instructions that share lines, and
+// nontemporal loads there fell from 5.37 to 3.43 TB/s.
+template <class V>
+__device__ __forceinline__ V ld_stream(const V* p) {
+    if constexpr (sizeof(V) == 16) {
+        using U = unsigned __attribute__((ext_vector_type(4)));
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
+    } else if constexpr (sizeof(V) == 8) {
+        using U = unsigned __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
+    } else if constexpr (sizeof(V) == 4) {
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p)));
+    } else {
+        return *p;
+    }
+}
+
 // Partials of a split axis are combined by reduce_finalize_kernel, a second launch on the same
 // stream.  (Combining them inside the first launch needs a device-scope release per block; on
 // this multi-XCD part that is an L2 write-back, which costs more than the extra launch.)
@@ -115,6 +135,7 @@ __device__ __forceinline__ void rows_body(OutOf<DT, OP>* __restrict__ out, const
     using V = VecT<S, VEC>;
     using St = typename R::St;
     constexpr int GPB = 256 / L;                         // groups per block
+    constexpr bool NT = L * sizeof(V) >= 128;            // a group's load covers whole lines
     const uint32_t group = bx * GPB + threadIdx.x / L;
     const uint32_t lane = threadIdx.x % L;
     const uint32_t ngroups = gx * GPB;
@@ -134,7 +155,10 @@ __device__ __forceinline__ void rows_body(OutOf<DT, OP>* __restrict__ out, const
             V v[U];
 #pragma unroll
             for (int u = 0; u < U; u++)
-                if (valid[u]) v[u] = *reinterpret_cast<const V*>(row[u] + e);
+                if (valid[u]) {
+                    const V* p = reinterpret_cast<const V*>(row[u] + e);
+                    v[u] = NT ? ld_stream(p) : *p;
+                }
 #pragma unroll
             for (int u = 0; u < U; u++)
                 if (valid[u]) {
@@ -178,6 +202,50 @@ __device__ __forceinline__ void lane_body(OutOf<DT, OP>* __restrict__ out, const
     out[g] = R::out(st);
 }
 
+// ------------------------------------------------------------------ lane, packed rows
+// Rows of nv <= 4 vectors stored back to back (input offset of output g is g * n): a block's 256
+// rows are one run of 256 * nv vectors.  It is read with whole-line streaming loads (vector f of
+// the run by thread f % 256), staged in LDS, and each lane then reduces its own row from LDS in the
+// order of lane_body, so both give the same bits.  LDS position of vector f: f ^ ((f >> 4) & mask)
+// with mask 3 for nv = 4 and 1 for nv = 2, which moves the chunks within their row so the 16 lanes
+// of one 128-bit LDS read pass hit distinct banks (nv = 3 and 1 need no swizzle).
+// smem: 1024 vectors (16 KiB).
+template <int DT, int OP, int VEC>
+__device__ __forceinline__ void lane_packed_body(OutOf<DT, OP>* __restrict__ out, const ElemOf<DT>* __restrict__ in,
+                                                 uint32_t total_out, uint32_t nv, uint32_t bx, void* smem) {
+    using R = typename RedSel<DT, OP>::R;
+    using S = ElemOf<DT>;
+    using V = VecT<S, VEC>;
+    V* sh = static_cast<V*>(smem);
+    const uint32_t g0 = bx * 256;
+    const uint32_t rows = min(256u, total_out - g0);
+    const uint32_t nvec = rows * nv;
+    const uint32_t mask = nv == 4 ? 3u : nv == 2 ? 1u : 0u;
+    const V* src = reinterpret_cast<const V*>(in) + (uint64_t)g0 * nv;
+    const uint32_t t = threadIdx.x;
+    V v[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+        if (t + 256u * w < nvec) v[w] = ld_stream(src + t + 256u * w);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t f = t + 256u * w;
+        if (f < nvec) sh[f ^ ((f >> 4) & mask)] = v[w];
+    }
+    __syncthreads();
+    if (t >= rows) return;
+    typename R::St st = R::init();
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+        if (u < (int)nv) {
+            const uint32_t f = t * nv + u;
+            const V x = sh[f ^ ((f >> 4) & mask)];
+#pragma unroll
+            for (int k = 0; k < VEC; k++) R::step(st, x.v[k], u * VEC + k);
+        }
+    out[g0 + t] = R::out(st);
+}
+
 
 // ------------------------------------------------------------------ block (stride 1, long rows)
 // One block of 64 * WAVES threads per (output g, chunk c).  U vectors per lane are in flight; the
@@ -200,7 +268,7 @@ __device__ __forceinline__ void block_body(OutOf<DT, OP>* __restrict__ out, StOf
     for (; e + (U - 1) * STEP < end; e += U * STEP) {
         V v[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const V*>(row + e + u * STEP);
+        for (int u = 0; u < U; u++) v[u] = ld_stream(reinterpret_cast<const V*>(row + e + u * STEP));
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
@@ -210,7 +278,7 @@ __device__ __forceinline__ void block_body(OutOf<DT, OP>* __restrict__ out, StOf
         V v[U - 1];
 #pragma unroll
         for (int u = 0; u < U - 1; u++)
-            if (e + u * STEP < end) v[u] = *reinterpret_cast<const V*>(row + e + u * STEP);
+            if (e + u * STEP < end) v[u] = ld_stream(reinterpret_cast<const V*>(row + e + u * STEP));
 #pragma unroll
         for (int u = 0; u < U - 1; u++)
             if (e + u * STEP < end) {
@@ -262,7 +330,7 @@ __device__ __forceinline__ void cols_body(OutOf<DT, OP>* __restrict__ out, StOf<
         for (; i + (U - 1) * WAVES < end; i += U * WAVES) {
             V v[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)(i + u * WAVES) * rs);
+            for (int u = 0; u < U; u++) v[u] = ld_stream(reinterpret_cast<const V*>(base + (uint64_t)(i + u * WAVES) * rs));
 #pragma unroll
             for (int u = 0; u < U; u++)
 #pragma unroll
@@ -272,7 +340,7 @@ __device__ __forceinline__ void cols_body(OutOf<DT, OP>* __restrict__ out, StOf<
             V v[U - 1];
 #pragma unroll
             for (int u = 0; u < U - 1; u++)
-                if (i + u * WAVES < end) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)(i + u * WAVES) * rs);
+                if (i + u * WAVES < end) v[u] = ld_stream(reinterpret_cast<const V*>(base + (uint64_t)(i + u * WAVES) * rs));
 #pragma unroll
             for (int u = 0; u < U - 1; u++)
                 if (i + u * WAVES < end) {
@@ -322,7 +390,7 @@ __device__ __forceinline__ void short_body(OutOf<DT, OP>* __restrict__ out, cons
     V v[NMAX];
 #pragma unroll
     for (int u = 0; u < NMAX; u++)
-        if (u < n) v[u] = *reinterpret_cast<const V*>(base + (uint64_t)u * rs);
+        if (u < n) v[u] = ld_stream(reinterpret_cast<const V*>(base + (uint64_t)u * rs));
     typename R::St st[VEC];
 #pragma unroll
     for (int k = 0; k < VEC; k++) st[k] = R::init();
@@ -386,6 +454,7 @@ struct Plan {
     int unroll = 1;         // rows plan: outputs in flight per lane group
     int waves = 1;          // cols / block / short plans: waves per block
     uint32_t nv = 0;        // lane plan: vectors per row
+    bool packed = false;    // lane plan: rows back to back (offset of output g is g * n), vector loads
     uint32_t blocks = 0;    // rows plan: grid size; cols plan: column groups
     uint32_t rounds = 0;
     uint32_t nsplit = 1;    // blocks sharing one output's axis
@@ -421,6 +490,9 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
         }
         if (p.mode == kLane) {
             p.blocks = (uint32_t)((tot + 255) / 256);
+            p.packed = p.vec == VEC && d.so[d.cd - 1] == 1;
+            for (int i = 0; p.packed && i < d.cd; i++)
+                if ((uint64_t)d.si[i] != (uint64_t)d.n * d.so[i]) p.packed = false;
         } else if (nv > 1024) {
             // One block per output when there are enough outputs to cover the CUs (no partials,
             // no cross-block step); otherwise split each row into chunks of >= 4 vectors a thread.

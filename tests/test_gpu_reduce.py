@@ -290,6 +290,37 @@ def test_plans_lane_short_and_tails(mx, orc, dt, shape, axis, opn):
         assert np.array_equal(bits(got), bits(ref)), (dt, shape, axis, opn)
 
 
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16", "INT32"])
+@pytest.mark.parametrize("nv", [1, 2, 3, 4])
+@pytest.mark.parametrize("opn", OPS)
+def test_lane_plan_packed_and_gapped_rows(mx, orc, dt, nv, opn):
+    """Rows of nv 16-byte vectors stored back to back (the block's rows are loaded as one run and
+    staged in LDS) and the same rows with a one-vector gap after each (one lane loads its own row):
+    both must give the oracle's bits, with a partial last block of rows."""
+    code, op = getattr(mx, dt), getattr(mx, opn)
+    vec = 16 // np.dtype(mx.NP_DTYPE[code]).itemsize
+    n = nv * vec
+    rng = np.random.default_rng(nv * 31 + code)
+    for rows in (3, 256, 1000):
+        xf = np.round(rng.standard_normal([rows, n + vec]) * 4).astype(np.float32)
+        if code == mx.FLOAT16:
+            xg = xf.astype(np.float16)
+        elif code == mx.BFLOAT16:
+            from oracle.oracle import f32_to_bf16_bits
+            xg = f32_to_bf16_bits(xf)
+        elif code == mx.INT32:
+            xg = xf.astype(np.int32)
+        else:
+            xg = xf
+        xp = np.ascontiguousarray(xg[:, :n])
+        got_p, ref_p, *_ = run_reduce(mx, orc, op, code, xp.ravel(), [rows, n], 1)
+        got_g, ref_g, *_ = run_reduce(mx, orc, op, code, xg.ravel(), [rows, n], 1, in_strides=[n + vec, 1])
+        # integer-valued inputs: float sums are exact, so every op is bit-exact
+        assert np.array_equal(bits(got_p), bits(ref_p)), (dt, nv, rows, opn, "packed")
+        assert np.array_equal(bits(got_g), bits(ref_g)), (dt, nv, rows, opn, "gapped")
+        assert np.array_equal(bits(got_p), bits(got_g)), (dt, nv, rows, opn)
+
+
 @pytest.mark.parametrize("opn", OPS)
 def test_unaligned_input_and_output(mx, orc, opn):
     """Views at a 4-byte offset: scalar loads for the lane / short plans, scalar output stores."""
