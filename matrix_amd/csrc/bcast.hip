@@ -46,7 +46,7 @@ template <int DT, int OP, int VEC, bool AV, bool BV>
 __global__ __launch_bounds__(kBlock) void bcast_vec_kernel(
     typename dt_traits<DT>::S* __restrict__ R, const typename dt_traits<DT>::S* __restrict__ A,
     const typename dt_traits<DT>::S* __restrict__ B, uint32_t nvec, FastDiv inner_vecs,
-    OuterDesc od) {
+    OuterDesc od, int nt) {
     using S = typename dt_traits<DT>::S;
     using V = Vec<S, VEC>;
     const uint32_t base = blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
@@ -70,11 +70,17 @@ __global__ __launch_bounds__(kBlock) void bcast_vec_kernel(
             orr += (uint64_t)idx * od.sR[d];
         }
         offR[u] = orr + col;
-        if constexpr (AV) va[u] = *reinterpret_cast<const V*>(A + oa + col);
+        if constexpr (AV) {
+            const V* p = reinterpret_cast<const V*>(A + oa + col);
+            va[u] = (nt & 1) ? ld_stream(p) : *p;
+        }
         else { S s = A[oa];
 #pragma unroll
             for (int i = 0; i < VEC; i++) va[u].v[i] = s; }
-        if constexpr (BV) vb[u] = *reinterpret_cast<const V*>(B + ob + col);
+        if constexpr (BV) {
+            const V* p = reinterpret_cast<const V*>(B + ob + col);
+            vb[u] = (nt & 2) ? ld_stream(p) : *p;
+        }
         else { S s = B[ob];
 #pragma unroll
             for (int i = 0; i < VEC; i++) vb[u].v[i] = s; }
@@ -146,12 +152,19 @@ int launch_typed(int cdims, const uint32_t* shape, const uint32_t* sR, const uin
         uint32_t nvec = (uint32_t)(total / VEC);
         dim3 grid((nvec + kBlock * kUnroll - 1) / (kBlock * kUnroll));
         FastDiv iv(inner / VEC);
+        // an operand that no axis broadcasts is read once: nontemporal loads
+        bool sa = sA[in] == 1, sb = sB[in] == 1;
+        for (int d = 0; d < in; d++) {
+            if (shape[d] > 1 && sA[d] == 0) sa = false;
+            if (shape[d] > 1 && sB[d] == 0) sb = false;
+        }
+        const int nt = (sa ? 1 : 0) | (sb ? 2 : 0);
         if (sA[in] == 1 && sB[in] == 1)
-            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, true, true>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od);
+            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, true, true>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od, nt);
         else if (sA[in] == 1)
-            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, true, false>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od);
+            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, true, false>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od, nt);
         else
-            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, false, true>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od);
+            hipLaunchKernelGGL((bcast_vec_kernel<DT, OP, VEC, false, true>), grid, dim3(kBlock), 0, st, R, A, B, nvec, iv, od, nt);
     } else {
         FullDesc fd{};
         fd.n = cdims;

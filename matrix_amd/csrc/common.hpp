@@ -162,4 +162,21 @@ struct DimArr {
     uint32_t v[N];
 };
 
+// Nontemporal (streaming) load of one 4-, 8- or 16-byte value, for inputs that are read once by
+// load instructions that each cover whole 128-byte lines; other sizes load normally.
+template <class V>
+__device__ __forceinline__ V ld_stream(const V* p) {
+    if constexpr (sizeof(V) == 16) {
+        using U = unsigned __attribute__((ext_vector_type(4)));
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
+    } else if constexpr (sizeof(V) == 8) {
+        using U = unsigned __attribute__((ext_vector_type(2)));
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
+    } else if constexpr (sizeof(V) == 4) {
+        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p)));
+    } else {
+        return *p;
+    }
+}
+
 }  // namespace mx

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256) void bcast_reduce_rows_kernel(typename dt_trai
                                                                 const typename dt_traits<DT>::S* __restrict__ B,
                                                                 typename RedSel<DT, ROP>::R::OutT* __restrict__ out,
                                                                 uint32_t rows, uint32_t nv, FastDiv inner_vecs,
-                                                                FuseDesc fd, int a_vec, int b_vec) {
+                                                                FuseDesc fd, int a_vec, int b_vec, int nt) {
     using S = typename dt_traits<DT>::S;
     using Red = typename RedSel<DT, ROP>::R;
     constexpr int VEC = 16 / sizeof(S);
@@ -64,13 +64,19 @@ __global__ __launch_bounds__(256) void bcast_reduce_rows_kernel(typename dt_trai
                 oa += (uint64_t)idx * fd.sA[d];
                 ob += (uint64_t)idx * fd.sB[d];
             }
-            if (a_vec) va[u] = *reinterpret_cast<const V*>(A + oa + col);
+            if (a_vec) {
+                const V* p = reinterpret_cast<const V*>(A + oa + col);
+                va[u] = (nt & 1) ? ld_stream(p) : *p;
+            }
             else {
                 const S x = A[oa];
 #pragma unroll
                 for (int k = 0; k < VEC; k++) va[u].v[k] = x;
             }
-            if (b_vec) vb[u] = *reinterpret_cast<const V*>(B + ob + col);
+            if (b_vec) {
+                const V* p = reinterpret_cast<const V*>(B + ob + col);
+                vb[u] = (nt & 2) ? ld_stream(p) : *p;
+            }
             else {
                 const S x = B[ob];
 #pragma unroll
@@ -123,9 +129,16 @@ bool launch_fast(int op, int red_op, int cdims, const uint32_t* shape, const uin
     const dim3 grid((rows + 3) / 4);
     const FastDiv iv(shape[in] / VEC);
     const int av = sA[in] == 1, bv = sB[in] == 1;
+    // an operand that no axis broadcasts is read once: nontemporal loads
+    bool sa = av, sb = bv;
+    for (int d = 0; d < in; d++) {
+        if (shape[d] > 1 && sA[d] == 0) sa = false;
+        if (shape[d] > 1 && sB[d] == 0) sb = false;
+    }
+    const int nt = (sa ? 1 : 0) | (sb ? 2 : 0);
     using OutT = S;
 #define MX_FUSE(BOP, ROP) hipLaunchKernelGGL((bcast_reduce_rows_kernel<DT, BOP, ROP>), grid, dim3(256), 0, st, (S*)R, \
-                                             (const S*)A, (const S*)B, (OutT*)out, rows, n / VEC, iv, fd, av, bv)
+                                             (const S*)A, (const S*)B, (OutT*)out, rows, n / VEC, iv, fd, av, bv, nt)
 #define MX_FUSE_R(BOP) do { switch (red_op) { case MX_RED_SUM: MX_FUSE(BOP, MX_RED_SUM); break; \
                                               case MX_RED_MAX: MX_FUSE(BOP, MX_RED_MAX); break; \
                                               default: MX_FUSE(BOP, MX_RED_MIN); break; } } while (0)

@@ -65,25 +65,10 @@ struct OffDesc {
 template <typename S, int VEC>
 struct alignas(VEC * sizeof(S) >= 16 ? 16 : VEC * sizeof(S)) VecT { S v[VEC]; };
 
-// Streaming loads of the reduced input (read exactly once), for plans whose load instructions
-// each cover whole 128-byte lines: nontemporal loads raise the axis-1 and axis-0 reductions of a
-// [256, 65536] f32 input from 5.80 to 6.24 TB/s and from 5.74 to 6.40 TB/s.  The lane plan keeps
-// ordinary loads: each lane's row is split over several load instructions that share lines, and
-// nontemporal loads there fell from 5.37 to 3.43 TB/s.
-template <class V>
-__device__ __forceinline__ V ld_stream(const V* p) {
-    if constexpr (sizeof(V) == 16) {
-        using U = unsigned __attribute__((ext_vector_type(4)));
-        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
-    } else if constexpr (sizeof(V) == 8) {
-        using U = unsigned __attribute__((ext_vector_type(2)));
-        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
-    } else if constexpr (sizeof(V) == 4) {
-        return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p)));
-    } else {
-        return *p;
-    }
-}
+// The coalesced plans read their input with ld_stream (nontemporal loads, common.hpp): the axis-1
+// and axis-0 reductions of a [256, 65536] f32 input rise from 5.80 to 6.24 TB/s and from 5.74 to
+// 6.40 TB/s.  The gapped lane plan keeps ordinary loads: each lane's row is split over several load
+// instructions that share lines, and nontemporal loads there fell from 5.37 to 3.43 TB/s.
 
 // Partials of a split axis are combined by reduce_finalize_kernel, a second launch on the same
 // stream.  (Combining them inside the first launch needs a device-scope release per block; on
