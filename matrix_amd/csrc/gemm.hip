@@ -88,17 +88,24 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(typename MmaTraits<DT>:
 
 // ------------------------------------------------------------------ skinny products (M <= 16)
 // A block owns 16 consecutive Bt rows (16 C columns) of one batch; its waves split the K range
-// into contiguous pieces.  Each step a lane loads one 16-byte K fragment of Bt row (n0 + l % 16)
-// and the same K fragment of A row (l % 16), at K offset 4 (l / 16) fragments, and a 16 x 16 MFMA
-// takes Bt as its row operand and A as its column operand: the result is the C^T tile, lane l
-// holding C[l % 16][n0 + 4 (l / 16) + r] in acc[r].  Rows past N or M are clamped to a valid row:
-// they only feed result rows / columns that are never stored.  Bt streams from HBM once; A (at
-// most 16 rows) is re-read from the caches.
-// The K loop is a rolling pipeline of U fragment slots: a slot is refilled with the step U ahead
-// right after its MFMA, so U steps stay in flight per wave.  Refills past the wave's last full
-// step re-read that step (a cache hit) and are discarded.  A last partial step (K not a multiple
-// of 4 fragments) is loaded with per-lane zero fill.  The waves' partial tiles are summed in wave
-// order through LDS (deterministic).
+// into contiguous pieces.  A step is 64 bytes of K: lane l takes the 16-byte K fragment
+// 4 (l / 16) + {0..3} of Bt row (n0 + l % 16) and of A row (l % 16), and a 16 x 16 MFMA takes Bt
+// as its row operand and A as its column operand: the result is the C^T tile, lane l holding
+// C[l % 16][n0 + 4 (l / 16) + r] in acc[r].  Rows past N or M are clamped to a valid row: they
+// only feed result rows / columns that are never stored.  Bt streams from HBM once; A (at most 16
+// rows) is re-read from the caches.
+//
+// Each wave streams its K range in chunks of 512 bytes of each of the block's 16 Bt rows.  A chunk
+// is read by 8 load instructions that each cover 512 contiguous bytes of 2 rows (whole lines,
+// nontemporal: Bt is read once), written to the wave's own 8 KiB of LDS, and the fragments are
+// read back from there.  (Loading the fragments straight from global memory makes every load
+// instruction touch 64 bytes of 16 rows; that form streamed 3.66 TB/s on A[8, 4096] x
+// Bt[4096, 4096] in f32 against 4.13 here.)  LDS position of 16-byte chunk c of row r: r * 32 + (c ^ r), so
+// the 16 rows of one fragment read fall in distinct banks.  The chunk's A fragments are loaded
+// before the next chunk's Bt loads are issued, so waiting for them never waits for the prefetch.
+// Per wave: two accumulators alternating by step, summed at the end, then the waves' tiles are
+// summed in wave order through LDS (deterministic).
+
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 template <int DT> struct SkinnyFrag;
@@ -106,11 +113,10 @@ template <> struct SkinnyFrag<MX_FLOAT32> { using V = f4v; };
 template <> struct SkinnyFrag<MX_FLOAT16> { using V = tile::h8v; };
 template <> struct SkinnyFrag<MX_BFLOAT16> { using V = tile::b8v; };
 
-// Waves per block and steps in flight per wave, per element size (measured on the skinny
-// workload: fewer requests in flight per CU stream faster when every load instruction touches 16
-// different Bt rows): fp32 8 waves x 4 steps, 16-bit 4 waves x 4 steps.
-template <int DT> constexpr int kSkinnyWaves = DT == MX_FLOAT32 ? 8 : 4;
-constexpr int kSkinnySteps = 4;
+// Waves per block (measured on A[8|16, K] x Bt[4096|8192, K], K = 4096 | 8192, for 4, 8 and 16
+// waves and for 512- and 1024-byte chunks: 8 waves of 512-byte chunks were fastest or within 3%
+// everywhere; rotating the waves' K ranges from block to block changed nothing).
+constexpr int kSkinnyWaves = 8;
 
 template <int DT>
 __device__ __forceinline__ f4v skinny_mma(typename SkinnyFrag<DT>::V b, typename SkinnyFrag<DT>::V a, f4v acc) {
@@ -126,21 +132,38 @@ __device__ __forceinline__ f4v skinny_mma(typename SkinnyFrag<DT>::V b, typename
     }
 }
 
-// kw: K elements per wave (a multiple of one step, 4 fragments).  CVEC: C columns are unit-stride
-// and every 4-column group starts 4-element aligned, so a lane's 4 results go out in one store.
+// The skinny path applies to 16-bit and fp32 data with unit K strides, 16-byte aligned rows and
+// K a whole number of fragments, at most 16 rows of A, and enough column tiles to fill the CUs.
+template <int DT>
+bool skinny_ok(const GemmArgs& g, const void* A, const void* Bt) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr uint32_t CE = 16 / sizeof(S);
+    if (g.M > 16 || g.ka != 1 || g.kb != 1 || g.K % CE || g.lda % CE || g.ldb % CE) return false;
+    if ((uintptr_t)A % 16 || (uintptr_t)Bt % 16 || g.batches > 65535) return false;
+    for (int d = 0; d < g.bd.n; d++)
+        if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
+    return (uint64_t)((g.N + 15) / 16) * g.batches >= 128;
+}
+
+// kw: K elements per wave (a multiple of one step).  CVEC: C columns are unit-stride and every
+// 4-column group starts 4-element aligned, so a lane's 4 results go out in one store.
 template <int DT, bool CVEC>
-__global__ __launch_bounds__(64 * kSkinnyWaves<DT>) void gemm_skinny_kernel(typename MmaTraits<DT>::S* __restrict__ C,
-                                                                        const typename MmaTraits<DT>::S* __restrict__ A,
-                                                                        const typename MmaTraits<DT>::S* __restrict__ Bt,
-                                                                        GemmArgs g, uint32_t kw) {
+__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
+    typename MmaTraits<DT>::S* __restrict__ C, const typename MmaTraits<DT>::S* __restrict__ A,
+    const typename MmaTraits<DT>::S* __restrict__ Bt, GemmArgs g, uint32_t kw) {
     using S = typename MmaTraits<DT>::S;
     using V = typename SkinnyFrag<DT>::V;
     constexpr uint32_t CE = 16 / sizeof(S);      // elements per fragment
-    constexpr uint32_t KS = 4 * CE;               // K per step
-    constexpr int U = kSkinnySteps;
-    constexpr int W = kSkinnyWaves<DT>;
+    constexpr uint32_t KS = 4 * CE;               // K per step (64 bytes of a row)
+    constexpr uint32_t CH = 8;                    // steps per chunk (512 bytes of a row)
+    constexpr uint32_t KC = CH * KS;
+    constexpr uint32_t CPR = CH * 4;              // 16-byte pieces per row of a chunk
+    constexpr uint32_t RPI = 64 / CPR;            // rows per load instruction
+    constexpr uint32_t NL = 16 / RPI;             // load instructions per chunk
+    constexpr int W = kSkinnyWaves;
+    __shared__ V stage[W][16 * CPR];
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t i = lane & 15, grp = lane >> 4;
     const uint32_t n0 = blockIdx.x * 16;
     uint32_t b = blockIdx.y;
@@ -153,57 +176,64 @@ __global__ __launch_bounds__(64 * kSkinnyWaves<DT>) void gemm_skinny_kernel(type
         offB += (uint64_t)idx * g.bd.sB[d];
         offC += (uint64_t)idx * g.bd.sC[d];
     }
-    const S* brow = Bt + offB + (uint64_t)min(n0 + i, g.N - 1) * g.ldb + grp * CE;
-    const S* arow = A + offA + (uint64_t)min(i, g.M - 1) * g.lda + grp * CE;
     const uint32_t kbeg = min(g.K, wave * kw);
     const uint32_t kend = min(g.K, kbeg + kw);
-    const uint32_t nfull = (kend - kbeg) / KS;              // full steps of this wave
-    f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-    if (nfull > 0) {
-        const S* bw = brow + kbeg;
-        const S* aw = arow + kbeg;
-        const uint32_t last = (nfull - 1) * KS;
-        V fb[U], fa[U];
-        // slot order in the prologue as in the loop, so on entry slot u is the u-th oldest load
+    const uint32_t lr = lane / CPR, lq = lane % CPR;
+    const S* bbase = Bt + offB;
+    uint64_t lrow[NL];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const uint32_t o = min((uint32_t)u * KS, last);
-            fb[u] = *reinterpret_cast<const V*>(bw + o);
-            fa[u] = *reinterpret_cast<const V*>(aw + o);
+    for (int j = 0; j < (int)NL; j++) lrow[j] = (uint64_t)min(n0 + RPI * j + lr, g.N - 1) * g.ldb;
+    const S* arow = A + offA + (uint64_t)min(i, g.M - 1) * g.lda;
+    V* st = stage[wave];
+    const V zero = {};
+    V R[NL], fa[CH];
+    f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+    // Every load is unconditional: an element at or beyond kend is read from element kbeg of the
+    // same row instead (in bounds) and replaced by zero where it is used, so no branch separates
+    // the loads and each wait names exactly the loads it needs.
+    auto load_chunk = [&](uint32_t kc) __attribute__((always_inline)) {
+        const uint32_t e = kc + lq * CE;
+        const uint32_t ee = e < kend ? e : kbeg;
+#pragma unroll
+        for (int j = 0; j < (int)NL; j++) R[j] = ld_stream(reinterpret_cast<const V*>(bbase + lrow[j] + ee));
+    };
+    auto stage_and_load_a = [&](uint32_t kc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < (int)NL; j++) {
+            const uint32_t r = RPI * j + lr;
+            st[r * CPR + (lq ^ r)] = R[j];
+        }
+#pragma unroll
+        for (int s = 0; s < (int)CH; s++) {
+            const uint32_t k = kc + s * KS + grp * CE;
+            fa[s] = *reinterpret_cast<const V*>(arow + (k < kend ? k : kbeg));
+        }
+    };
+    auto compute = [&](uint32_t kc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < (int)CH; s++) {
+            const bool ok = kc + s * KS + grp * CE < kend;
+            const V fb = st[i * CPR + ((s * 4 + grp) ^ i)];
+            if (s & 1) acc1 = skinny_mma<DT>(ok ? fb : zero, ok ? fa[s] : zero, acc1);
+            else acc0 = skinny_mma<DT>(ok ? fb : zero, ok ? fa[s] : zero, acc0);
+        }
+    };
+    const uint32_t nch = kend > kbeg ? (kend - kbeg + KC - 1) / KC : 0;
+    if (nch > 0) {
+        load_chunk(kbeg);
+        for (uint32_t c = 0; c + 1 < nch; c++) {
+            const uint32_t kc = kbeg + c * KC;
+            // issue order: stage + A loads, then the next chunk's Bt loads, then the MFMAs
+            stage_and_load_a(kc);
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk(kc + KC);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(kc);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // whole rounds of U steps: no branch inside, so each MFMA waits only for its own slot
-        const uint32_t rounds = nfull / U;
-        for (uint32_t r = 0; r < rounds; r++) {
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                if (u & 1) acc1 = skinny_mma<DT>(fb[u], fa[u], acc1);
-                else acc0 = skinny_mma<DT>(fb[u], fa[u], acc0);
-                const uint32_t o = min(((r + 1) * U + u) * KS, last);
-                fb[u] = *reinterpret_cast<const V*>(bw + o);
-                fa[u] = *reinterpret_cast<const V*>(aw + o);
-            }
-            // keep the order slot by slot: its MFMAs (mask 0x008), then its two refills (0x020),
-            // so the refill of slot u is in flight while slots u + 1 .. are consumed
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, DT == MX_FLOAT32 ? 4 : 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-            }
-        }
-        // the remaining nfull % U steps were loaded by the last round's refills
-        const uint32_t rem = nfull % U;
-#pragma unroll
-        for (int u = 0; u < U; u++)
-            if ((uint32_t)u < rem) acc0 = skinny_mma<DT>(fb[u], fa[u], acc0);
-    }
-    const uint32_t kt = kbeg + nfull * KS;                 // partial last step, if any
-    if (kt < kend) {
-        const bool ok = kt + grp * CE < kend;
-        const V zero = {};
-        const V bv = ok ? *reinterpret_cast<const V*>(brow + kt) : zero;
-        const V av = ok ? *reinterpret_cast<const V*>(arow + kt) : zero;
-        acc0 = skinny_mma<DT>(bv, av, acc0);
+        const uint32_t kc = kbeg + (nch - 1) * KC;
+        stage_and_load_a(kc);
+        compute(kc);
     }
     f4v acc = acc0 + acc1;
     __shared__ f4v part[W - 1][64];
@@ -223,7 +253,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves<DT>) void gemm_skinny_kernel(type
         else o[r] = float_to_bf16(acc[r]);
     }
     if constexpr (CVEC) {
-        if (nb < g.N) {              // N % 4 == 0 on this path: the whole group is in range
+        if (nb < g.N) {
             struct alignas(4 * sizeof(S)) Q { S v[4]; } q{{o[0], o[1], o[2], o[3]}};
             *reinterpret_cast<Q*>(crow + nb) = q;
         }
@@ -234,24 +264,11 @@ __global__ __launch_bounds__(64 * kSkinnyWaves<DT>) void gemm_skinny_kernel(type
     }
 }
 
-// The skinny path applies to 16-bit and fp32 data with unit K strides, 16-byte aligned rows and
-// K a whole number of fragments, at most 16 rows of A, and enough column tiles to fill the CUs.
-template <int DT>
-bool skinny_ok(const GemmArgs& g, const void* A, const void* Bt) {
-    using S = typename MmaTraits<DT>::S;
-    constexpr uint32_t CE = 16 / sizeof(S);
-    if (g.M > 16 || g.ka != 1 || g.kb != 1 || g.K % CE || g.lda % CE || g.ldb % CE) return false;
-    if ((uintptr_t)A % 16 || (uintptr_t)Bt % 16 || g.batches > 65535) return false;
-    for (int d = 0; d < g.bd.n; d++)
-        if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
-    return (uint64_t)((g.N + 15) / 16) * g.batches >= 128;
-}
-
 template <int DT>
 int launch_skinny(const GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
     using S = typename MmaTraits<DT>::S;
     constexpr uint32_t KS = 4 * (16 / sizeof(S));
-    constexpr int W = kSkinnyWaves<DT>;
+    constexpr int W = kSkinnyWaves;
     uint32_t kw = (g.K + W - 1) / W;
     kw = (kw + KS - 1) / KS * KS;
     bool cvec = g.cn == 1 && g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)C % (4 * sizeof(S)) == 0;
