@@ -161,6 +161,21 @@ int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC,
                              const uint32_t* sA, const uint32_t* sBt, const uint32_t* sC,
                              uint32_t K, void* C, const void* A, const void* Bt, void* stream);
 
+/* No counterpart in the reference: a Dot node followed by a broadcast Add of a bias row and a
+ * Max / Min against a scalar (DotPrimitive, primitives.cpp:5464-5626; AdditionPrimitive,
+ * primitives.cpp:397-560; MaxPrimitive / MinPrimitive, primitives.cpp:2515-2824), the bias +
+ * ReLU of a dense layer, in one call for a graph compiler that fuses the three nodes.  Computes
+ * C as mx_launch_batched_matmul does, then Z = C + bias (bias: N contiguous elements, broadcast
+ * over the batch and M) and H = max(Z, s) (act_op MX_OP_MAX) or min(Z, s) (MX_OP_MIN), s one
+ * element at act_scalar, each element exactly as mx_launch_bcast_binary computes it, so C, Z
+ * and H equal those three launches bit for bit.  float32 / float16 / bfloat16; C, Z and H
+ * contiguous with C's shape.  With a split K range the combine launch writes C, Z and H; else
+ * one epilogue launch reads C once and writes Z and H. */
+int mx_launch_batched_matmul_bias_act(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                      const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
+                                      const void* A, const void* Bt, const void* bias, void* Z, int act_op,
+                                      const void* act_scalar, void* H, void* stream);
+
 /* Channels-last N-D convolution, the argument set of conv_gpu (Matrix.mm:12335-12395) /
  * conv2d_gpu (Matrix.mm:5521-5559): input [N, S1..Sn, C], kernel [O, K1..Kn, C/groups],
  * output [N, O1..On, O], each with arbitrary element strides; pad_lo / stride / dil_rhs

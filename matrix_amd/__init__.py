@@ -91,6 +91,8 @@ _SIGS = {
     "mx_broadcast_shapes": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_broadcast_shapes_matmul": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_launch_batched_matmul": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp], _i),
+    "mx_launch_batched_matmul_bias_act": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp, _vp, _i,
+                                           _vp, _vp, _vp], _i),
     "mx_conv_workspace_bytes": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _i, ctypes.POINTER(_sz)], _i),
     "mx_launch_conv_nd": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _ip, _ip, _ip, _ip,
                            _i, _i, _vp, _vp, _vp, _vp, _sz, _vp], _i),
@@ -320,6 +322,15 @@ def launch_batched_matmul(dtype, desc, K, C, A, Bt, stream=None):
     shape, sA, sBt, sC = desc
     check(lib.mx_launch_batched_matmul(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
                                        int(C), int(A), int(Bt), stream))
+
+
+def launch_batched_matmul_bias_act(dtype, desc, K, C, A, Bt, bias, Z, act_op, act_scalar, H, stream=None):
+    """C = A . Bt^T, Z = C + bias (N elements), H = act_op(Z, *act_scalar) (OP_MAX / OP_MIN) in one
+    call; desc as for launch_batched_matmul, C / Z / H contiguous."""
+    shape, sA, sBt, sC = desc
+    check(lib.mx_launch_batched_matmul_bias_act(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
+                                                int(C), int(A), int(Bt), int(bias), int(Z), act_op,
+                                                int(act_scalar), int(H), stream))
 
 
 def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=0, workspace_bytes=0,

@@ -13,6 +13,7 @@
 // When Bt is shared by the whole batch (batch stride 0) and A / C stack their batches
 // contiguously, the batch folds into M.
 #include "mfma_tile.hpp"
+#include "elementwise.hpp"
 
 namespace mx {
 namespace {
@@ -57,17 +58,48 @@ __global__ __launch_bounds__(256) void gemm_scalar_kernel(typename dt_traits<DT>
     }
 }
 
-// Split-K combine: C[b, m, n] = round(sum over s of P[s][b][m][n]), splits in order.
+// Bias + activation epilogue of mx_launch_batched_matmul_bias_act: Z = C + bias[n] and
+// H = act(Z, s), elementwise as the broadcast Add and Max / Min kernels compute them, written at
+// C's offsets.
+struct Epi {
+    void* Z;
+    void* H;
+    const void* bias;       // N elements
+    const void* s;          // one element
+    int act;                // MX_OP_MAX or MX_OP_MIN
+};
+
 template <int DT>
+__device__ __forceinline__ void epi_store(const Epi& e, uint64_t off, uint32_t n, typename MmaTraits<DT>::S c) {
+    using S = typename MmaTraits<DT>::S;
+    const S z = BinOp<DT, MX_OP_ADD>::apply(c, static_cast<const S*>(e.bias)[n]);
+    const S sv = *static_cast<const S*>(e.s);
+    static_cast<S*>(e.Z)[off] = z;
+    static_cast<S*>(e.H)[off] = e.act == MX_OP_MAX ? BinOp<DT, MX_OP_MAX>::apply(z, sv) : BinOp<DT, MX_OP_MIN>::apply(z, sv);
+}
+
+// Split-K combine: C[b, m, n] = round(sum over s of P[s][b][m][n]), splits in order (EPI: and the
+// bias + activation epilogue from the rounded C).
+template <int DT, bool EPI>
 __global__ __launch_bounds__(256) void splitk_sum_kernel(typename MmaTraits<DT>::S* __restrict__ C,
                                                          const float* __restrict__ P, uint32_t nsplit, GemmArgs g,
-                                                         FastDiv fn, FastDiv fm) {
+                                                         FastDiv fn, FastDiv fm, Epi e) {
     using S = typename MmaTraits<DT>::S;
     const uint64_t per = (uint64_t)g.batches * g.M * g.N;
     const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= per) return;
+    // splits added in order; 8 loads issued before their adds (many splits of a small C are
+    // otherwise one memory latency each)
     float acc = P[t];
-    for (uint32_t s = 1; s < nsplit; s++) acc += P[(uint64_t)s * per + t];
+    uint32_t s = 1;
+    for (; s + 8 <= nsplit; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = P[(uint64_t)(s + j) * per + t];
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc += v[j];
+    }
+    for (; s < nsplit; s++) acc += P[(uint64_t)s * per + t];
     const uint32_t tt = (uint32_t)t;                     // the launcher keeps per < 2^32
     uint32_t q = fn.div(tt);
     const uint32_t n = tt - q * g.N;
@@ -83,7 +115,51 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(typename MmaTraits<DT>:
     if constexpr (DT == MX_FLOAT32) v = acc;
     else if constexpr (DT == MX_FLOAT16) v = float_to_half_bits(acc);
     else v = float_to_bf16(acc);
-    C[offC + (uint64_t)m * g.ldc + (uint64_t)n * g.cn] = v;
+    const uint64_t off = offC + (uint64_t)m * g.ldc + (uint64_t)n * g.cn;
+    C[off] = v;
+    if constexpr (EPI) epi_store<DT>(e, off, n, v);
+}
+
+// The epilogue after an unsplit product: C, Z and H contiguous, VEC consecutive elements of one
+// row per thread (N % VEC == 0, 16-byte aligned buffers), else one element.
+template <int DT, int VEC>
+__global__ __launch_bounds__(256) void bias_act_kernel(const typename MmaTraits<DT>::S* __restrict__ C, Epi e,
+                                                       uint64_t total, FastDiv fnv) {
+    using S = typename MmaTraits<DT>::S;
+    struct alignas(VEC * sizeof(S)) Vv { S v[VEC]; };
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t * VEC >= total) return;
+    const uint32_t tv = (uint32_t)t;                      // total / VEC < 2^32 (checked by the launcher)
+    const uint32_t n0 = (tv - fnv.div(tv) * fnv.d) * VEC;
+    const Vv c = reinterpret_cast<const Vv*>(C)[t];
+    const S* bias = static_cast<const S*>(e.bias);
+    const S sv = *static_cast<const S*>(e.s);
+    Vv z, h;
+#pragma unroll
+    for (int k = 0; k < VEC; k++) {
+        z.v[k] = BinOp<DT, MX_OP_ADD>::apply(c.v[k], bias[n0 + k]);
+        h.v[k] = e.act == MX_OP_MAX ? BinOp<DT, MX_OP_MAX>::apply(z.v[k], sv) : BinOp<DT, MX_OP_MIN>::apply(z.v[k], sv);
+    }
+    reinterpret_cast<Vv*>(e.Z)[t] = z;
+    reinterpret_cast<Vv*>(e.H)[t] = h;
+}
+
+template <int DT>
+int launch_bias_act(const GemmArgs& g, const void* C, const Epi& e, hipStream_t st) {
+    using S = typename MmaTraits<DT>::S;
+    constexpr int VEC = 16 / sizeof(S);
+    const uint64_t total = (uint64_t)g.batches * g.M * g.N;
+    const bool vec = g.N % VEC == 0 && (uintptr_t)C % 16 == 0 && (uintptr_t)e.Z % 16 == 0 && (uintptr_t)e.H % 16 == 0;
+    if (vec) {
+        const uint64_t nt = total / VEC;
+        hipLaunchKernelGGL((bias_act_kernel<DT, VEC>), dim3((uint32_t)((nt + 255) / 256)), dim3(256), 0, st, (const S*)C,
+                           e, total, FastDiv(g.N / VEC));
+    } else {
+        hipLaunchKernelGGL((bias_act_kernel<DT, 1>), dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, (const S*)C,
+                           e, total, FastDiv(g.N));
+    }
+    MX_HIP(hipGetLastError());
+    return MX_OK;
 }
 
 // ------------------------------------------------------------------ skinny products (M <= 16)
@@ -301,10 +377,13 @@ uint32_t choose_split(const tile::TileShape& ts, const GemmArgs& g, uint32_t pai
 }
 
 template <int DT>
-int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
+int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st, const Epi* epi = nullptr) {
     using S = typename MmaTraits<DT>::S;
     constexpr int CE = 16 / sizeof(S);
-    if (skinny_ok<DT>(g, A, Bt)) return launch_skinny<DT>(g, C, A, Bt, st);
+    if (skinny_ok<DT>(g, A, Bt)) {
+        const int rc = launch_skinny<DT>(g, C, A, Bt, st);
+        return rc || !epi ? rc : launch_bias_act<DT>(g, C, *epi, st);
+    }
     const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
     uint32_t ksplit = 0;
     const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
@@ -346,15 +425,23 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t
             rc = vec ? tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit)
                      : tile::launch_tile_kernel<DT, false, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit);
         if (rc) return rc;
-        hipLaunchKernelGGL((splitk_sum_kernel<DT>), dim3((uint32_t)((per + 255) / 256)), dim3(256), 0, st, (S*)C,
-                           (const float*)P, nsplit, g, FastDiv(g.N), FastDiv(g.M));
+        const dim3 grid((uint32_t)((per + 255) / 256));
+        if (epi)
+            hipLaunchKernelGGL((splitk_sum_kernel<DT, true>), grid, dim3(256), 0, st, (S*)C, (const float*)P, nsplit, g,
+                               FastDiv(g.N), FastDiv(g.M), *epi);
+        else
+            hipLaunchKernelGGL((splitk_sum_kernel<DT, false>), grid, dim3(256), 0, st, (S*)C, (const float*)P, nsplit, g,
+                               FastDiv(g.N), FastDiv(g.M), Epi{});
         MX_HIP(hipGetLastError());
         return MX_OK;
     }
+    int rc = -1;
     if constexpr (DT == MX_FLOAT32)
-        if (nn) return tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc, true>(ts, g, geo, C, A, Bt, st, who);
-    if (vec) return tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
-    return tile::launch_tile_kernel<DT, false, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
+        if (nn) rc = tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc, true>(ts, g, geo, C, A, Bt, st, who);
+    if (rc < 0)
+        rc = vec ? tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who)
+                 : tile::launch_tile_kernel<DT, false, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
+    return rc || !epi ? rc : launch_bias_act<DT>(g, C, *epi, st);
 }
 
 template <int DT>
@@ -374,13 +461,16 @@ int launch_scalar(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream
 
 using namespace mx;
 
-extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
-                                        const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
-                                        const void* A, const void* Bt, void* stream) {
+namespace {
+
+// Fills g from the collapsed descriptor (mx_launch_batched_matmul's arguments).  Returns MX_OK,
+// a failure status, or -1 when there is nothing to compute.
+int matmul_args(const char* who, int cdims, const uint32_t* shapeC, const uint32_t* sA, const uint32_t* sBt,
+                const uint32_t* sC, uint32_t K, void* C, const void* A, const void* Bt, GemmArgs& g) {
     if (cdims < 2 || cdims > MX_MAX_DIMS)
-        return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: cdims " + std::to_string(cdims) + " outside [2, 8]");
-    if (!shapeC || !sA || !sBt || !sC) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: null descriptor");
-    GemmArgs g{};
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": cdims " + std::to_string(cdims) + " outside [2, 8]");
+    if (!shapeC || !sA || !sBt || !sC) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": null descriptor");
+    g = GemmArgs{};
     g.M = shapeC[cdims - 2];
     g.N = shapeC[cdims - 1];
     g.K = K;
@@ -392,10 +482,10 @@ extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* sh
     g.cn = sC[cdims - 1];
     uint64_t batches = 1;
     for (int d = 0; d < cdims - 2; d++) batches *= shapeC[d];
-    if (batches == 0 || g.M == 0 || g.N == 0) return MX_OK;
+    if (batches == 0 || g.M == 0 || g.N == 0) return -1;
     if (batches * g.M > 0xffffffffull || batches * g.N > 0xffffffffull)
-        return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: extent above 2^32-1 (size_m indexing)");
-    if (!C || ((!A || !Bt) && K > 0)) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: null buffer");
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": extent above 2^32-1 (size_m indexing)");
+    if (!C || ((!A || !Bt) && K > 0)) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": null buffer");
     // Fold the batch into M when Bt is shared by every batch and A and C stack their batches as
     // consecutive row blocks (one batch axis, A stride M*lda, C stride M*ldc).
     g.bd.n = cdims - 2;
@@ -410,6 +500,17 @@ extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* sh
         g.batches = 1;
         g.bd.n = 0;
     }
+    return MX_OK;
+}
+
+}  // namespace
+
+extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                        const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
+                                        const void* A, const void* Bt, void* stream) {
+    GemmArgs g;
+    const int ar = matmul_args("mx_launch_batched_matmul", cdims, shapeC, sA, sBt, sC, K, C, A, Bt, g);
+    if (ar) return ar < 0 ? MX_OK : ar;
     hipStream_t st;
     if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
     switch (dtype) {
@@ -427,5 +528,37 @@ extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* sh
     case MX_BOOL: return launch_scalar<MX_BOOL>(g, C, A, Bt, st);
     default:
         return fail(MX_ERR_UNSUPPORTED, "mx_launch_batched_matmul: no kernel for dtype " + std::to_string(dtype));
+    }
+}
+
+extern "C" int mx_launch_batched_matmul_bias_act(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                                 const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
+                                                 const void* A, const void* Bt, const void* bias, void* Z,
+                                                 int act_op, const void* act_scalar, void* H, void* stream) {
+    const char* who = "mx_launch_batched_matmul_bias_act";
+    if (dtype != MX_FLOAT32 && dtype != MX_FLOAT16 && dtype != MX_BFLOAT16)
+        return fail(MX_ERR_UNSUPPORTED, std::string(who) + ": float32 / float16 / bfloat16 only, dtype " +
+                                            std::to_string(dtype));
+    if (act_op != MX_OP_MAX && act_op != MX_OP_MIN)
+        return fail(MX_ERR_INVALID_ARG, std::string(who) + ": act_op must be MX_OP_MAX or MX_OP_MIN");
+    GemmArgs g;
+    const int ar = matmul_args(who, cdims, shapeC, sA, sBt, sC, K, C, A, Bt, g);
+    if (ar) return ar < 0 ? MX_OK : ar;
+    // C (and so Z and H) contiguous: the epilogue walks them linearly
+    uint64_t want = 1;
+    for (int d = cdims - 1; d >= 0; --d) {
+        if (shapeC[d] != 1 && sC[d] != want)
+            return fail(MX_ERR_INVALID_ARG, std::string(who) + ": C must be contiguous");
+        want *= shapeC[d];
+    }
+    if (want > 0xffffffffull) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": more than 2^32-1 outputs");
+    if (!bias || !Z || !act_scalar || !H) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": null buffer");
+    hipStream_t st;
+    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+    const Epi e{Z, H, bias, act_scalar, act_op};
+    switch (dtype) {
+    case MX_FLOAT32: return launch_mfma<MX_FLOAT32>(g, C, A, Bt, st, &e);
+    case MX_FLOAT16: return launch_mfma<MX_FLOAT16>(g, C, A, Bt, st, &e);
+    default: return launch_mfma<MX_BFLOAT16>(g, C, A, Bt, st, &e);
     }
 }

@@ -257,6 +257,31 @@ struct ViewPrim : Primitive {
     }
 };
 
+// Execute generation of the calling thread: run_schedule advances it once per execute.
+thread_local uint64_t t_exec_gen = 0;
+
+// A Dot node that also produces Max|Min(Add(Dot, bias), s): the dense layer's bias + ReLU.  The
+// Max / Min node registers it at compile time (BinaryPrim::try_fuse_epilogue); the Dot's
+// execute then launches mx_launch_batched_matmul_bias_act, which writes the Dot's, the Add's
+// and the Max's outputs, and records the execute it did so in.  The Add and the Max skip their
+// own launch only in that same execute.  The Add's and the Max's storage is held weakly (those
+// nodes hold the Dot, not the other way round); bias and s are leaves.
+struct DotEpilogue {
+    matrix bias, s;
+    std::weak_ptr<matrix_amd::Storage> z, h;
+    int act = MX_OP_MAX;
+    uint64_t gen = 0;
+};
+
+// MATRIX_AMD_FUSE_EPILOGUE=0 compiles Dot / Add / Max as three launches.
+bool epilogue_fusion_on() {
+    static const bool on = [] {
+        const char* e = std::getenv("MATRIX_AMD_FUSE_EPILOGUE");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on;
+}
+
 // Broadcast binary op (and Equal): out = a op b with NumPy broadcasting.
 // When a reduction over this node's last axis is compiled against it (ReducePrim::compile), the
 // node also produces that reduction: execute() launches mx_launch_bcast_binary_reduce_rows, which
@@ -272,6 +297,7 @@ struct BinaryPrim : Primitive {
     int fused_red_op = -1;
     uint32_t fused_n = 0;
     uint64_t fused_runs = 0;
+    std::shared_ptr<DotEpilogue> epi_of;            // this Add / Max is part of a Dot's epilogue
     BinaryPrim(int o, matrix x, matrix y) : op(o), a(std::move(x)), b(std::move(y)) {}
     const char* name() const override {
         static const char* n[] = {"Add", "Sub", "Mul", "Divide", "Max", "Min", "Equal"};
@@ -285,8 +311,11 @@ struct BinaryPrim : Primitive {
                                   b2t), "broadcast");
         if (out.dims == 0) { cd = 0; return; }
         check(mx_collapse_dims3(os, b1t, b2t, ost, out.dims, kCap, cs, sA, sB, sR, &cd), "collapse_dims");
+        try_fuse_epilogue(out);
     }
+    void try_fuse_epilogue(const matrix& out);
     void execute(const matrix& out) override {
+        if (epi_of && epi_of->gen == t_exec_gen) return;   // the Dot's launch wrote this output just now
         if (auto red = fused_out.lock(); red && red->dev && fused_red_op >= 0) {
             check(mx_launch_bcast_binary_reduce_rows(op, fused_red_op, (int)a.type, (int)cd, cs, sR, sA, sB, fused_n,
                                                      dptr(out), dptr(a), dptr(b), red->dev, stream),
@@ -359,7 +388,8 @@ struct ReducePrim : Primitive {
     // 16 KiB, no split workspace) and the producer has no fused reduction yet.
     void try_fuse(const matrix& out) {
         auto* bp = dynamic_cast<BinaryPrim*>(in.tape.get());
-        if (!bp || bp->fused_red_op >= 0 || in.dims == 0 || axis != (int)in.dims - 1 || ws.bytes || n == 0) return;
+        if (!bp || bp->fused_red_op >= 0 || bp->epi_of || in.dims == 0 || axis != (int)in.dims - 1 || ws.bytes || n == 0)
+            return;
         if (!in.is_contiguous() || in.offset != 0 || (uint64_t)n * dtype_size(in.type) > 16384) return;
         bp->fused_out = out.storage;
         bp->fused_red_op = op;
@@ -387,6 +417,7 @@ struct DotPrim : Primitive {
     matrix a, bt;
     uint32_t cd = 0, K = 0;
     uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sC[MX_MAX_DIMS];
+    std::shared_ptr<DotEpilogue> epi;
     DotPrim(matrix x, matrix y) : a(std::move(x)), bt(std::move(y)) {}
     const char* name() const override { return "Dot"; }
     uint32_t num_inputs() const override { return 2; }
@@ -404,6 +435,19 @@ struct DotPrim : Primitive {
         }
     }
     void execute(const matrix& out) override {
+        if (epi) {
+            auto z = epi->z.lock(), h = epi->h.lock();
+            const auto& bs = epi->bias.storage;
+            const auto& ss = epi->s.storage;
+            if (z && h && z->dev && h->dev && bs->dev && !bs->dev_stale && ss->dev && !ss->dev_stale) {
+                check(mx_launch_batched_matmul_bias_act((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a),
+                                                        dptr(bt), dptr(epi->bias), z->dev, epi->act, dptr(epi->s),
+                                                        h->dev, stream),
+                      "launch Dot + bias + activation");
+                epi->gen = t_exec_gen;
+                return;
+            }
+        }
         check(mx_launch_batched_matmul((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a), dptr(bt), stream),
               "launch Dot");
     }
@@ -417,6 +461,35 @@ struct DotPrim : Primitive {
         return {ga.unbroadcast_shape(a.shape(), a.dims), gb.unbroadcast_shape(bt.shape(), bt.dims)};
     }
 };
+
+// Max|Min(Add(Dot(...), bias), s) with bias and s leaves: the Dot launches all three (bias a row
+// of N elements broadcast over the Dot's other axes, s one element, one float dtype throughout).
+void BinaryPrim::try_fuse_epilogue(const matrix& out) {
+    if ((op != MX_OP_MAX && op != MX_OP_MIN) || !epilogue_fusion_on()) return;
+    const int ty = (int)out.type;
+    if (ty != MX_FLOAT32 && ty != MX_FLOAT16 && ty != MX_BFLOAT16) return;
+    if (b.tape || b.total_size() != 1 || b.type != out.type || fused_red_op >= 0) return;
+    auto* add = dynamic_cast<BinaryPrim*>(a.tape.get());
+    if (!add || add->op != MX_OP_ADD || add->epi_of || add->fused_red_op >= 0) return;
+    auto* dot = dynamic_cast<DotPrim*>(add->a.tape.get());
+    if (!dot || dot->epi) return;
+    const matrix& t = add->a;
+    const matrix& bias = add->b;
+    if (t.type != out.type || bias.type != out.type || bias.tape || !bias.is_contiguous() || bias.offset != 0) return;
+    if (t.dims < 2 || t.shape_vec() != a.shape_vec() || a.shape_vec() != out.shape_vec()) return;
+    if (!t.is_contiguous() || t.offset != 0 || !a.is_contiguous() || a.offset != 0) return;
+    const size_m N = t.shape()[t.dims - 1];
+    if (bias.dims < 1 || bias.dims > t.dims || bias.shape()[bias.dims - 1] != N || bias.total_size() != N) return;
+    auto e = std::make_shared<DotEpilogue>();
+    e->bias = bias;
+    e->s = b;
+    e->z = a.storage;
+    e->h = out.storage;
+    e->act = op;
+    dot->epi = e;
+    add->epi_of = e;
+    epi_of = e;
+}
 
 // Strided copy with cast into a contiguous output.
 struct CopyPrim : Primitive {
@@ -1013,6 +1086,7 @@ bool schedule_holds(const Schedule& sc, const std::vector<matrix>& ms) {
 }
 
 void run_schedule(const Schedule& sc, Executor& ex) {
+    t_exec_gen++;
     for (const matrix& l : sc.leaves)
         if (l.storage->dev_stale) l.storage->upload();      // leaf written on the host
     const auto& nodes = sc.nodes;

@@ -213,6 +213,61 @@ CASE(gpu_fused_reduction_lifecycle) {
     }
 }
 
+// A dense layer's bias + ReLU, h = max(x . W + b, 0): the Dot launches the product, the bias Add
+// and the Max together (mx_launch_batched_matmul_bias_act).  t, z and h must hold the product,
+// z = t + b and h = max(z, 0) exactly (from the downloaded t), on the first run, after the bias
+// and x change on the host, and when only h is executed.
+CASE(gpu_dense_bias_relu_lifecycle) {
+    const size_m R = 64, K = 96, N = 256;
+    auto xv = randn((size_t)R * K, 40);
+    auto wv = randn((size_t)K * N, 41);
+    auto bv = randu(N, 42, -1.f, 1.f);
+    matrix x = matrix::from_host<float>({R, K}, xv);
+    matrix W = matrix::from_host<float>({K, N}, wv);
+    matrix b = matrix::from_host<float>({N}, bv);
+    matrix t = x.dot(W);
+    matrix z = t + b;
+    matrix h = matrix::max(z, matrix::scalar(0.0f));
+    std::vector<matrix> outs{t, z, h};
+    auto check = [&](const std::vector<float>& xx, const std::vector<float>& bb, const char* when) {
+        auto tg = t.to_host<float>();
+        auto zg = z.to_host<float>();
+        auto hg = h.to_host<float>();
+        size_t clamped = 0;
+        for (size_t r = 0; r < R; r++)
+            for (size_t j = 0; j < N; j++) {
+                double ref = 0, mag = 0;
+                for (size_t k = 0; k < K; k++) {
+                    ref += (double)xx[r * K + k] * wv[k * N + j];
+                    mag += std::fabs((double)xx[r * K + k] * wv[k * N + j]);
+                }
+                const size_t i = r * N + j;
+                EXPECT(std::fabs(tg[i] - ref) <= 1e-5 * mag + 1e-6, std::string("product ") + when);
+                const float zr = tg[i] + bb[j];
+                EXPECT(zg[i] == zr, std::string("bias add ") + when);
+                EXPECT(hg[i] == ((zr < 0.0f) ? 0.0f : zr), std::string("relu ") + when);
+                clamped += hg[i] != zg[i];
+            }
+        EXPECT(clamped > 0 && clamped < (size_t)R * N, std::string("relu clamps some ") + when);
+    };
+    matrix::compile_gpu(outs);
+    matrix::execute_gpu(outs);
+    check(xv, bv, "first run");
+    auto bv2 = randu(N, 43, -2.f, 2.f);            // new bias: z and h must follow it
+    std::memcpy(b.host_data(), bv2.data(), bv2.size() * sizeof(float));
+    b.mark_changed();
+    matrix::clear_trace_checks(outs);
+    matrix::execute_gpu(outs);
+    check(xv, bv2, "after the bias changed");
+    auto xv2 = randn((size_t)R * K, 44);          // new input, only h requested
+    std::memcpy(x.host_data(), xv2.data(), xv2.size() * sizeof(float));
+    x.mark_changed();
+    std::vector<matrix> only_h{h};
+    matrix::clear_trace_checks(only_h);
+    matrix::execute_gpu(only_h);
+    check(xv2, bv2, "executing h alone");
+}
+
 // Independent reductions with one descriptor run as group launches (horizontal fusion): five over
 // axis 1, three over axis 0, two over axis 3 of a reshape and the two chained over axis 1 after
 // them.  d reduces with the axis-0 descriptor but depends on one of that group's members, so it
@@ -529,6 +584,7 @@ int main(int argc, char** argv) {
     } else {
         run("gpu_add_then_rowsum", gpu_add_then_rowsum);
         run("gpu_fused_reduction_lifecycle", gpu_fused_reduction_lifecycle);
+        run("gpu_dense_bias_relu_lifecycle", gpu_dense_bias_relu_lifecycle);
         run("gpu_grouped_reductions", gpu_grouped_reductions);
         run("gpu_reductions_and_views", gpu_reductions_and_views);
         run("gpu_dot_batched_broadcast", gpu_dot_batched_broadcast);
