@@ -151,6 +151,17 @@ int mx_launch_bcast_binary_reduce_rows(int op, int red_op, int dtype, int cdims,
                                        const uint32_t* sR, const uint32_t* sA, const uint32_t* sB, uint32_t n,
                                        void* R, const void* A, const void* B, void* out, void* stream);
 
+/* No counterpart in the reference: the gradient that the vjp of Max / Min (MaxPrimitive /
+ * MinPrimitive, primitives.cpp:2604-2608) sends to one operand, built there from four nodes:
+ * mask_b = equal(b, max(a, b)) (min for MX_OP_MIN), then R = G * (1 - mask_b) for side 0 (a)
+ * or R = G * mask_b for side 1 (b), in one launch for a graph's backward pass.  The arrays are
+ * the CollapsedDims_3 of R = broadcast(A, B) as for mx_launch_bcast_binary; G is read with R's
+ * strides.  float32 / float16 / bfloat16; each element equals the four broadcast launches'
+ * result bit for bit. */
+int mx_launch_max_grad(int op, int side, int dtype, int cdims, const uint32_t* shape, const uint32_t* sR,
+                       const uint32_t* sA, const uint32_t* sB, void* R, const void* A, const void* B,
+                       const void* G, void* stream);
+
 /* C[b, m, n] = sum_k A[b, m, k] * Bt[b, n, k].  Replaces dot_gpu / batched_dot_gpu
  * (Matrix.mm:7198-7291).  The arrays are exactly CollapsedDims_3 from collapse_dims_matmul
  * (Mods/Utils.mm:204-252): shapeC = [batch..., M, N], sA / sBt / sC per axis, whose last

@@ -91,6 +91,7 @@ _SIGS = {
     "mx_broadcast_shapes": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_broadcast_shapes_matmul": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_launch_batched_matmul": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp], _i),
+    "mx_launch_max_grad": ([_i, _i, _i, _i, _u32p, _u32p, _u32p, _u32p, _vp, _vp, _vp, _vp, _vp], _i),
     "mx_launch_batched_matmul_bias_act": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp, _vp, _i,
                                            _vp, _vp, _vp], _i),
     "mx_conv_workspace_bytes": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _i, ctypes.POINTER(_sz)], _i),
@@ -322,6 +323,14 @@ def launch_batched_matmul(dtype, desc, K, C, A, Bt, stream=None):
     shape, sA, sBt, sC = desc
     check(lib.mx_launch_batched_matmul(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
                                        int(C), int(A), int(Bt), stream))
+
+
+def launch_max_grad(op, side, dtype, desc, R, A, B, G, stream=None):
+    """Gradient of Max / Min (op) to operand a (side 0) or b (side 1): desc as for
+    launch_bcast_binary, G read with R's strides."""
+    shape, sA, sB, sR = desc
+    check(lib.mx_launch_max_grad(op, side, dtype, len(shape), u32(shape), u32(sR), u32(sA), u32(sB), int(R), int(A),
+                                 int(B), int(G), stream))
 
 
 def launch_batched_matmul_bias_act(dtype, desc, K, C, A, Bt, bias, Z, act_op, act_scalar, H, stream=None):

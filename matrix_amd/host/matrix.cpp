@@ -282,6 +282,47 @@ bool epilogue_fusion_on() {
     return on;
 }
 
+// MATRIX_AMD_FUSE_MAXGRAD=0 keeps the four-node vjp of Max / Min.
+bool maxgrad_fusion_on() {
+    static const bool on = [] {
+        const char* e = std::getenv("MATRIX_AMD_FUSE_MAXGRAD");
+        return !e || std::atoi(e) != 0;
+    }();
+    return on;
+}
+
+// The gradient Max / Min send to one operand (side 0: a, side 1: b) as one node and one launch
+// (mx_launch_max_grad) in place of the four nodes of their vjp, max|min(a, b), equal(b, that),
+// 1 - mask and the product with g (primitives.cpp:2604-2608), with the same results bit for bit.
+// g is contiguous with the broadcast's shape, as R is.
+struct MaxGradPrim : Primitive {
+    int op, side;
+    matrix a, b, g;
+    uint32_t cd = 0;
+    uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sR[MX_MAX_DIMS];
+    MaxGradPrim(int o, int sd, matrix x, matrix y, matrix gg)
+        : op(o), side(sd), a(std::move(x)), b(std::move(y)), g(std::move(gg)) {}
+    const char* name() const override { return op == MX_OP_MAX ? "MaxGrad" : "MinGrad"; }
+    uint32_t num_inputs() const override { return 3; }
+    matrix& input_at(uint32_t i) override { return i == 0 ? a : i == 1 ? b : g; }
+    void compile(const matrix& out) override {
+        uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+        check(mx_broadcast_shapes(a.shape(), a.strides(), a.dims, b.shape(), b.strides(), b.dims, os, ost, b1s, b1t, b2s,
+                                  b2t), "broadcast");
+        if (out.dims == 0) { cd = 0; return; }
+        check(mx_collapse_dims3(os, b1t, b2t, ost, out.dims, kCap, cs, sA, sB, sR, &cd), "collapse_dims");
+    }
+    void execute(const matrix& out) override {
+        check(mx_launch_max_grad(op, side, (int)a.type, (int)cd, cs, sR, sA, sB, dptr(out), dptr(a), dptr(b), dptr(g),
+                                 stream), std::string("launch ") + name());
+    }
+    std::vector<matrix> vjp(matrix& gg) override {
+        matrix mb = matrix::equal(b, op == MX_OP_MAX ? matrix::max(a, b) : matrix::min(a, b));
+        matrix mask = side ? mb : 1.0f - mb;
+        return {a.zeros(), b.zeros(), gg * mask};
+    }
+};
+
 // Broadcast binary op (and Equal): out = a op b with NumPy broadcasting.
 // When a reduction over this node's last axis is compiled against it (ReducePrim::compile), the
 // node also produces that reduction: execute() launches mx_launch_bcast_binary_reduce_rows, which
@@ -314,6 +355,18 @@ struct BinaryPrim : Primitive {
         try_fuse_epilogue(out);
     }
     void try_fuse_epilogue(const matrix& out);
+    // g can feed one MaxGradPrim per operand: one float dtype, g contiguous with the broadcast shape
+    bool maxgrad_fusable(const matrix& g) const {
+        const int ty = (int)a.type;
+        if (!maxgrad_fusion_on() || (ty != MX_FLOAT32 && ty != MX_FLOAT16 && ty != MX_BFLOAT16)) return false;
+        if (b.type != a.type || g.type != a.type || !g.storage || !g.is_contiguous() || g.offset != 0) return false;
+        uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+        if (mx_broadcast_shapes(a.shape(), a.strides(), a.dims, b.shape(), b.strides(), b.dims, os, ost, b1s, b1t, b2s,
+                                b2t) != MX_OK)
+            return false;
+        const uint32_t nd = std::max(a.dims, b.dims);
+        return g.dims == nd && g.shape_vec() == std::vector<size_m>(os, os + nd);
+    }
     void execute(const matrix& out) override {
         if (epi_of && epi_of->gen == t_exec_gen) return;   // the Dot's launch wrote this output just now
         if (auto red = fused_out.lock(); red && red->dev && fused_red_op >= 0) {
@@ -340,6 +393,12 @@ struct BinaryPrim : Primitive {
         }
         case MX_OP_MAX:
         case MX_OP_MIN: {
+            if (maxgrad_fusable(g)) {
+                auto side = [&](int sd) {
+                    return matrix::make_node(g.shape_vec(), g.type, std::make_shared<MaxGradPrim>(op, sd, a, b, g));
+                };
+                return {side(0).unbroadcast_shape(as, a.dims), side(1).unbroadcast_shape(bs, b.dims)};
+            }
             // ties send the gradient to b (primitives.cpp:2604-2608)
             matrix mask_b = matrix::equal(b, op == MX_OP_MAX ? matrix::max(a, b) : matrix::min(a, b));
             matrix mask_a = 1.0f - mask_b;
