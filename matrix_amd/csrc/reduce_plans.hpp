@@ -462,6 +462,9 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
     const int VEC = (int)(16 / elem);
     const bool aligned = in_ptr % 16 == 0;
     if (tot == 0) return p;
+    // at most 64 KiB of input: one launch (a split would add a combine launch for microseconds
+    // of work)
+    const bool small = tot * d.n * elem <= 65536;
     if (d.rs == 1 && d.n > 1) {
         bool v_ok = VEC > 1 && d.n % VEC == 0;
         for (int i = 0; v_ok && i < d.cd; i++) if (d.si[i] % VEC) v_ok = false;
@@ -488,7 +491,7 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
             uint64_t want = (want_blocks + tot - 1) / tot;
             uint64_t maxc = (nv + threads * 4 - 1) / (threads * 4);
             uint64_t nc = want < maxc ? want : maxc;
-            if (nc < 1) nc = 1;
+            if (nc < 1 || small) nc = 1;
             uint32_t chunk_v = (uint32_t)((nv + nc - 1) / nc);
             p.chunk = chunk_v * nominal;
             p.nsplit = (d.n + p.chunk - 1) / p.chunk;
@@ -527,7 +530,7 @@ Plan make_plan(const Desc& d, size_t elem, size_t stbytes, uintptr_t in_ptr) {
     p.waves = 4;
     // split the axis over blocks when there are fewer column groups than CUs
     p.nsplit = 1;
-    if (groups < 256 && d.n >= 256) {
+    if (groups < 256 && d.n >= 256 && !small) {
         uint64_t want = (512 + groups - 1) / groups;
         uint64_t maxc = d.n / 128;                 // keep >= 128 axis elements per split
         if (maxc > 4096) maxc = 4096;

@@ -321,6 +321,20 @@ def test_lane_plan_packed_and_gapped_rows(mx, orc, dt, nv, opn):
         assert np.array_equal(bits(got_p), bits(got_g)), (dt, nv, rows, opn)
 
 
+@pytest.mark.parametrize("shape,axis", [([1, 5120], 1), ([5120], 0), ([512, 10], 0), ([2, 8192], 1), ([128, 128], 0)])
+@pytest.mark.parametrize("opn", OPS)
+def test_small_reductions_take_one_launch(mx, orc, shape, axis, opn):
+    """At most 64 KiB of input: no split of the axis (no workspace, no combine launch), same
+    results as the oracle (a loss, a bias gradient)."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(sum(shape) + axis)
+    x = np.round(rng.standard_normal(shape) * 4).astype(np.float32)
+    desc, rs, n, total = reduce_desc(mx, shape, axis)
+    assert mx.reduce_workspace_bytes(op, mx.FLOAT32, rs, n, desc) == 0
+    got, ref, *_ = run_reduce(mx, orc, op, mx.FLOAT32, x.ravel(), shape, axis)
+    assert np.array_equal(bits(got), bits(ref)), (shape, axis, opn)
+
+
 @pytest.mark.parametrize("opn", OPS)
 def test_unaligned_input_and_output(mx, orc, opn):
     """Views at a 4-byte offset: scalar loads for the lane / short plans, scalar output stores."""
