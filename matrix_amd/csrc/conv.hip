@@ -199,16 +199,16 @@ __global__ __launch_bounds__(256) void pack_input_transpose_kernel(S* __restrict
 // cover 128 contiguous bytes of one channel row (loads) or of one position row (stores).
 // Channels in [C, Cgp) are written as zeros.
 template <typename S>
-__global__ __launch_bounds__(256) void pack_input_transpose16_kernel(S* __restrict__ xp, const S* __restrict__ in,
-                                                                     uint32_t P, uint32_t C, uint32_t Cgp, uint64_t sN,
-                                                                     uint64_t sC) {
+__device__ __forceinline__ void pack_input_transpose16_body(S* __restrict__ xp, const S* __restrict__ in, uint32_t P,
+                                                            uint32_t C, uint32_t Cgp, uint64_t sN, uint64_t sC,
+                                                            uint32_t bx, uint32_t by, uint32_t bz) {
     constexpr int VE = 16 / sizeof(S);
     struct alignas(16) V { S v[VE]; };
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t c = blockIdx.y * (8 * VE) + (lane & 7) * VE;
-    const uint32_t p = (blockIdx.x * 32 + wave * 8 + (lane >> 3)) * VE;
+    const uint32_t c = by * (8 * VE) + (lane & 7) * VE;
+    const uint32_t p = (bx * 32 + wave * 8 + (lane >> 3)) * VE;
     if (p >= P || c >= Cgp) return;
-    const S* src = in + (uint64_t)blockIdx.z * sN + p;
+    const S* src = in + (uint64_t)bz * sN + p;
     // rows past C load a valid row (no branch between the loads) and are zeroed afterwards
     V v[VE];
 #pragma unroll
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(256) void pack_input_transpose16_kernel(S* __restri
 #pragma unroll
             for (int j = 0; j < VE; j++) v[i].v[j] = S(0);
         }
-    S* dst = xp + ((uint64_t)blockIdx.z * P + p) * Cgp + c;
+    S* dst = xp + ((uint64_t)bz * P + p) * Cgp + c;
 #pragma unroll
     for (int j = 0; j < VE; j++) {
         V w;
@@ -227,6 +227,13 @@ __global__ __launch_bounds__(256) void pack_input_transpose16_kernel(S* __restri
         for (int i = 0; i < VE; i++) w.v[i] = v[i].v[j];
         *reinterpret_cast<V*>(dst + (uint64_t)j * Cgp) = w;
     }
+}
+
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input_transpose16_kernel(S* __restrict__ xp, const S* __restrict__ in,
+                                                                     uint32_t P, uint32_t C, uint32_t Cgp, uint64_t sN,
+                                                                     uint64_t sC) {
+    pack_input_transpose16_body(xp, in, P, C, Cgp, sN, sC, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Wp[o, k.., c] = c < Cg ? kern[o, (flip ? K - 1 - k : k).., c] : 0.
@@ -241,10 +248,9 @@ struct PackKDesc {
 
 // The launcher keeps total below 2^32, so the index decomposes with 32-bit FastDiv.
 template <typename S>
-__global__ __launch_bounds__(256) void pack_kernel_kernel(S* __restrict__ wp, const S* __restrict__ kern,
-                                                          uint32_t total, PackKDesc d) {
-    const uint32_t stride = gridDim.x * 256;
-    for (uint32_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+__device__ __forceinline__ void pack_kernel_body(S* __restrict__ wp, const S* __restrict__ kern, uint32_t total,
+                                                 const PackKDesc& d, uint32_t first, uint32_t stride) {
+    for (uint32_t t = first; t < total; t += stride) {
         uint32_t rem = t;
         uint32_t q = d.dims[d.ns + 1].div(rem);
         const uint32_t c = rem - q * d.dims[d.ns + 1].d;
@@ -259,6 +265,31 @@ __global__ __launch_bounds__(256) void pack_kernel_kernel(S* __restrict__ wp, co
         off += (uint64_t)rem * d.s[0];
         wp[t] = c < d.Cg ? kern[off] : S(0);
     }
+}
+
+template <typename S>
+__global__ __launch_bounds__(256) void pack_kernel_kernel(S* __restrict__ wp, const S* __restrict__ kern,
+                                                          uint32_t total, PackKDesc d) {
+    pack_kernel_body(wp, kern, total, d, blockIdx.x * 256 + threadIdx.x, gridDim.x * 256);
+}
+
+// Both packs in one launch (a channel-major input and a kernel to pack, the reference's NCHW /
+// OIHW views), as a 1-D grid: the first nwb blocks pack the kernel, one element per thread; the
+// rest are the (gx, gy, N) blocks of pack_input_transpose16_kernel, x fastest.
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input16_and_kernel_kernel(S* __restrict__ xp, const S* __restrict__ in,
+                                                                      uint32_t P, uint32_t C, uint32_t Cgp, uint64_t sN,
+                                                                      uint64_t sC, uint32_t gx, uint32_t gy,
+                                                                      S* __restrict__ wp, const S* __restrict__ kern,
+                                                                      uint32_t wtotal, uint32_t nwb, PackKDesc d) {
+    const uint32_t b = blockIdx.x;
+    if (b < nwb) {
+        pack_kernel_body(wp, kern, wtotal, d, b * 256 + threadIdx.x, nwb * 256);
+        return;
+    }
+    const uint32_t r = b - nwb;
+    const uint32_t q = r / gx;
+    pack_input_transpose16_body(xp, in, P, C, Cgp, sN, sC, r - q * gx, q % gy, q / gy);
 }
 
 // ------------------------------------------------------------------ direct kernel
@@ -413,24 +444,39 @@ int read_shape(int dtype, int ns, const uint32_t* in_shape, const uint32_t* k_sh
     return MX_OK;
 }
 
-template <typename S>
-int launch_pack_input(const ConvShape& cs, uint32_t Cgp, S* xp, const S* in, hipStream_t st) {
-    // channel-major special case: the spatial axes collapse into one unit-stride run
+// Channel-major input (the spatial axes collapse into one unit-stride run).
+bool channel_major(const ConvShape& cs, uint64_t* P) {
     bool run = cs.groups == 1 && cs.in_s[cs.ns] == 1;
     for (int d = cs.ns - 1; d >= 1 && run; --d) run = cs.in_s[d] == cs.in_s[d + 1] * cs.S[d];
-    uint64_t P = 1;
-    for (int d = 0; d < cs.ns; d++) P *= cs.S[d];
+    *P = 1;
+    for (int d = 0; d < cs.ns; d++) *P *= cs.S[d];
+    return run && *P < (1ull << 31) && cs.N < 65536;
+}
+
+// The 16-byte transpose applies (positions, strides and buffers in whole 16-byte units): its grid.
+template <typename S>
+bool transpose16_grid(const ConvShape& cs, uint32_t Cgp, const S* xp, const S* in, dim3* grid, uint64_t* P) {
     constexpr uint32_t VE = 16 / sizeof(S);
-    if (run && P < (1ull << 31) && cs.N < 65536 && P % VE == 0 && cs.in_s[cs.ns + 1] % VE == 0 &&
-        cs.in_s[0] % VE == 0 && Cgp % VE == 0 && (uintptr_t)in % 16 == 0 && (uintptr_t)xp % 16 == 0) {
-        dim3 grid((uint32_t)((P + 32 * VE - 1) / (32 * VE)), (Cgp + 8 * VE - 1) / (8 * VE), cs.N);
+    if (!channel_major(cs, P) || *P % VE || cs.in_s[cs.ns + 1] % VE || cs.in_s[0] % VE || Cgp % VE ||
+        (uintptr_t)in % 16 || (uintptr_t)xp % 16)
+        return false;
+    *grid = dim3((uint32_t)((*P + 32 * VE - 1) / (32 * VE)), (Cgp + 8 * VE - 1) / (8 * VE), cs.N);
+    return true;
+}
+
+template <typename S>
+int launch_pack_input(const ConvShape& cs, uint32_t Cgp, S* xp, const S* in, hipStream_t st) {
+    uint64_t P;
+    dim3 grid;
+    if (transpose16_grid(cs, Cgp, xp, in, &grid, &P)) {
         hipLaunchKernelGGL((pack_input_transpose16_kernel<S>), grid, dim3(256), 0, st, xp, in, (uint32_t)P, cs.C, Cgp,
                            cs.in_s[0], cs.in_s[cs.ns + 1]);
         MX_HIP(hipGetLastError());
         return MX_OK;
     }
-    if (run && P < (1ull << 31) && cs.N < 65536) {
-        dim3 grid((uint32_t)((P + 63) / 64), (Cgp + 63) / 64, cs.N);
+    const bool run = channel_major(cs, &P);
+    if (run) {
+        grid = dim3((uint32_t)((P + 63) / 64), (Cgp + 63) / 64, cs.N);
         hipLaunchKernelGGL((pack_input_transpose_kernel<S>), grid, dim3(256), 0, st, xp, in, (uint32_t)P, cs.C, Cgp,
                            cs.in_s[0], cs.in_s[cs.ns + 1]);
         MX_HIP(hipGetLastError());
@@ -452,12 +498,11 @@ int launch_pack_input(const ConvShape& cs, uint32_t Cgp, S* xp, const S* in, hip
     return MX_OK;
 }
 
-template <typename S>
-int launch_pack_kernel(const ConvShape& cs, uint32_t Cgp, int flip, S* wp, const S* kern, hipStream_t st) {
-    PackKDesc d{};
+int pack_kernel_desc(const ConvShape& cs, uint32_t Cgp, int flip, PackKDesc& d, uint64_t& total) {
+    d = PackKDesc{};
     d.ns = cs.ns;
     d.dims[0] = FastDiv(cs.O);
-    uint64_t total = (uint64_t)cs.O * Cgp;
+    total = (uint64_t)cs.O * Cgp;
     for (int a = 0; a < cs.ns; a++) {
         d.dims[a + 1] = FastDiv(cs.K[a]);
         d.K[a] = cs.K[a];
@@ -468,6 +513,14 @@ int launch_pack_kernel(const ConvShape& cs, uint32_t Cgp, int flip, S* wp, const
     d.flip = flip;
     for (int a = 0; a < cs.ns + 2; a++) d.s[a] = cs.k_s[a];
     if (total > 0xffffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: kernel of 2^32 or more elements");
+    return MX_OK;
+}
+
+template <typename S>
+int launch_pack_kernel(const ConvShape& cs, uint32_t Cgp, int flip, S* wp, const S* kern, hipStream_t st) {
+    PackKDesc d;
+    uint64_t total;
+    if (int rc = pack_kernel_desc(cs, Cgp, flip, d, total)) return rc;
     const uint64_t want = (total + 255) / 256;
     hipLaunchKernelGGL((pack_kernel_kernel<S>), dim3((uint32_t)(want < 65536 ? want : 65536)), dim3(256), 0, st, wp,
                        kern, (uint32_t)total, d);
@@ -555,6 +608,27 @@ int launch_mfma_path(const ConvShape& cs, const Plan& p, const int* pad_lo, cons
     using S = typename MmaTraits<DT>::S;
     char* w = static_cast<char*>(ws);
     const void* xp = in;
+    if (p.pack_in && (p.pack_k || flip)) {
+        // both packs in one launch when the input takes the 16-byte transpose
+        S* xs = reinterpret_cast<S*>(w);
+        S* wsp = reinterpret_cast<S*>(w + p.xp_bytes);
+        uint64_t P;
+        dim3 grid;
+        if (transpose16_grid(cs, p.Cgp, xs, static_cast<const S*>(in), &grid, &P)) {
+            PackKDesc d;
+            uint64_t wtotal;
+            if (int rc = pack_kernel_desc(cs, p.Cgp, flip, d, wtotal)) return rc;
+            const uint64_t nwb = (wtotal + 255) / 256;
+            const uint64_t blocks = nwb + (uint64_t)grid.x * grid.y * grid.z;
+            if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: pack grid too large");
+            hipLaunchKernelGGL((pack_input16_and_kernel_kernel<S>), dim3((uint32_t)blocks), dim3(256), 0, st, xs,
+                               static_cast<const S*>(in), (uint32_t)P, cs.C, p.Cgp, cs.in_s[0], cs.in_s[cs.ns + 1],
+                               grid.x, grid.y, wsp, static_cast<const S*>(kern), (uint32_t)wtotal, (uint32_t)nwb, d);
+            MX_HIP(hipGetLastError());
+            if (cs.ns == 1) return launch_implicit_gemm<DT, 1>(cs, p.Cgp, pad_lo, stride, dil, out, xs, wsp, st);
+            return launch_implicit_gemm<DT, 2>(cs, p.Cgp, pad_lo, stride, dil, out, xs, wsp, st);
+        }
+    }
     if (p.pack_in) {
         int rc = launch_pack_input<S>(cs, p.Cgp, reinterpret_cast<S*>(w), static_cast<const S*>(in), st);
         if (rc) return rc;
