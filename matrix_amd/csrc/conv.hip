@@ -292,6 +292,41 @@ __global__ __launch_bounds__(256) void pack_input16_and_kernel_kernel(S* __restr
     pack_input_transpose16_body(xp, in, P, C, Cgp, sN, sC, r - q * gx, q % gy, q / gy);
 }
 
+// A 1 x 1 kernel with stride > 1 and no padding reads only the sampled positions: pack just
+// those, Xp[n, o.., c] = c < C ? in[n, (o * stride).., c] : 0, so the product runs at stride 1 on
+// a dense [N, OS.., Cgp] input.  Lane (cb = l % 8, pb = l / 8) of wave w takes output position
+// 32 x + 8 w + pb and the VE channels starting at (8 y + cb) VE: the 8 lanes of one position
+// store 128 contiguous bytes of its row, and the 8 positions of one channel read neighbouring
+// samples.  osd: FastDiv of the last output extent (2-D); ns = 1 or 2.
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input_sampled_kernel(S* __restrict__ xp, const S* __restrict__ in,
+                                                                 uint32_t OP, FastDiv osd, int ns, uint32_t C,
+                                                                 uint32_t Cgp, uint64_t sN, uint64_t sC, uint64_t s1,
+                                                                 uint64_t s2, uint32_t st1, uint32_t st2) {
+    constexpr int VE = 16 / sizeof(S);
+    struct alignas(16) V { S v[VE]; };
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = blockIdx.x * 32 + wave * 8 + (lane >> 3);
+    const uint32_t c0 = (blockIdx.y * 8 + (lane & 7)) * VE;
+    if (q >= OP || c0 >= Cgp) return;
+    uint64_t off;
+    if (ns == 2) {
+        const uint32_t oh = osd.div(q), ow = q - oh * osd.d;
+        off = (uint64_t)oh * st1 * s1 + (uint64_t)ow * st2 * s2;
+    } else {
+        off = (uint64_t)q * st1 * s1;
+    }
+    const S* src = in + (uint64_t)blockIdx.z * sN + off;
+    // channels past C load channel C - 1 (no branch between the loads) and are zeroed after
+    V v;
+#pragma unroll
+    for (int i = 0; i < VE; i++) v.v[i] = src[(uint64_t)min(c0 + i, C - 1) * sC];
+#pragma unroll
+    for (int i = 0; i < VE; i++)
+        if (c0 + i >= C) v.v[i] = S(0);
+    *reinterpret_cast<V*>(xp + ((uint64_t)blockIdx.z * OP + q) * Cgp + c0) = v;
+}
+
 // ------------------------------------------------------------------ direct kernel
 struct DirectDesc {
     int ns;
@@ -602,12 +637,49 @@ int launch_direct(const ConvShape& cs, const int* pad_lo, const int* stride, con
     return MX_OK;
 }
 
+// A 1 x 1 kernel, no padding, one group, a stride above 1, 16-byte aligned packed rows: the
+// sampled positions alone are packed (a quarter of the image at stride 2).
+bool sampled_1x1(const ConvShape& cs, const int* pad_lo, const int* stride) {
+    if (cs.groups != 1 || cs.ns < 1 || cs.ns > 2) return false;
+    bool strided = false;
+    for (int d = 0; d < cs.ns; d++) {
+        if (cs.K[d] != 1 || pad_lo[d] != 0 || stride[d] < 1) return false;
+        if ((uint64_t)(cs.OS[d] - 1) * stride[d] >= cs.S[d]) return false;
+        strided |= stride[d] > 1;
+    }
+    return strided;
+}
+
 template <int DT>
 int launch_mfma_path(const ConvShape& cs, const Plan& p, const int* pad_lo, const int* stride, const int* dil,
                      int flip, void* out, const void* in, const void* kern, void* ws, hipStream_t st) {
     using S = typename MmaTraits<DT>::S;
     char* w = static_cast<char*>(ws);
     const void* xp = in;
+    if (p.pack_in && sampled_1x1(cs, pad_lo, stride) && (uintptr_t)w % 16 == 0) {
+        // pack the sampled positions only, then a stride-1 product over them
+        S* xs = reinterpret_cast<S*>(w);
+        constexpr uint32_t VE = 16 / sizeof(S);
+        uint32_t OP = 1;
+        for (int d = 0; d < cs.ns; d++) OP *= cs.OS[d];
+        const dim3 grid((OP + 31) / 32, (p.Cgp + 8 * VE - 1) / (8 * VE), cs.N);
+        hipLaunchKernelGGL((pack_input_sampled_kernel<S>), grid, dim3(256), 0, st, xs, static_cast<const S*>(in), OP,
+                           FastDiv(cs.OS[cs.ns - 1]), cs.ns, cs.C, p.Cgp, cs.in_s[0], cs.in_s[cs.ns + 1], cs.in_s[1],
+                           cs.ns == 2 ? cs.in_s[2] : 0, (uint32_t)stride[0], cs.ns == 2 ? (uint32_t)stride[1] : 0u);
+        MX_HIP(hipGetLastError());
+        const void* wq = kern;
+        if (p.pack_k || flip) {
+            if (int rc = launch_pack_kernel<S>(cs, p.Cgp, flip, reinterpret_cast<S*>(w + p.xp_bytes),
+                                               static_cast<const S*>(kern), st))
+                return rc;
+            wq = w + p.xp_bytes;
+        }
+        ConvShape cd = cs;
+        for (int d = 0; d < cs.ns; d++) cd.S[d] = cs.OS[d];
+        const int one[kMaxSpatial] = {1, 1, 1, 1, 1, 1}, zero[kMaxSpatial] = {};
+        if (cs.ns == 1) return launch_implicit_gemm<DT, 1>(cd, p.Cgp, zero, one, one, out, xs, wq, st);
+        return launch_implicit_gemm<DT, 2>(cd, p.Cgp, zero, one, one, out, xs, wq, st);
+    }
     if (p.pack_in && (p.pack_k || flip)) {
         // both packs in one launch when the input takes the 16-byte transpose
         S* xs = reinterpret_cast<S*>(w);

@@ -116,6 +116,48 @@ def test_conv2d_mfma(mx, orc, dt, case):
     assert err <= TOL[dt], (dt, case, err)
 
 
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
+    # (N, C, H, W, O, stride_h, stride_w, layout): 1 x 1 kernels, no padding, stride > 1 -- only
+    # the sampled positions are packed, then a stride-1 product over them
+    (3, 20, 13, 11, 24, 3, 3, "nchw"),     # odd extents, channels zero-padded to the K pair
+    (2, 64, 9, 9, 16, 2, 2, "nhwc"),       # channels-last input with padded channels (f16: 64 -> 64)
+    (2, 48, 10, 12, 40, 2, 1, "nchw"),     # stride 2 along H only
+    (1, 16, 7, 16, 8, 1, 4, "nhwc"),       # stride 4 along W only
+])
+def test_conv2d_1x1_strided_sampled_pack(mx, orc, dt, case):
+    code = getattr(mx, dt)
+    n, c, h, w, o, sh, sw, layout = case
+    rng = np.random.default_rng(n * 31 + c + o)
+    if layout == "nchw":
+        x = store_of(code, rng.standard_normal([n, c, h, w]).astype(np.float32), mx)
+        in_shape, in_st = nchw_view(n, c, h, w)
+        wt = store_of(code, (rng.standard_normal([o, c, 1, 1]) * np.sqrt(2.0 / c)).astype(np.float32), mx)
+        k_shape, k_st = oihw_view(o, c, 1, 1)
+    else:
+        x = store_of(code, rng.standard_normal([n, h, w, c]).astype(np.float32), mx)
+        in_shape, in_st = [n, h, w, c], contiguous_strides([n, h, w, c])
+        wt = store_of(code, (rng.standard_normal([o, 1, 1, c]) * np.sqrt(2.0 / c)).astype(np.float32), mx)
+        k_shape, k_st = [o, 1, 1, c], contiguous_strides([o, 1, 1, c])
+    got, ref = run_conv(mx, orc, code, x, in_shape, in_st, wt, k_shape, k_st, [0, 0], [sh, sw])
+    err = normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx))
+    assert err <= TOL[dt], (dt, case, err)
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16"])
+def test_conv1d_1x1_strided_sampled_pack(mx, orc, dt):
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(17)
+    n, c, L, o, s = 3, 36, 101, 20, 3
+    x = store_of(code, rng.standard_normal([n, c, L]).astype(np.float32), mx)
+    st = contiguous_strides([n, c, L])
+    wt = store_of(code, (rng.standard_normal([o, 1, c]) * np.sqrt(2.0 / c)).astype(np.float32), mx)
+    got, ref = run_conv(mx, orc, code, x, [n, L, c], [st[0], st[2], st[1]], wt, [o, 1, c],
+                        contiguous_strides([o, 1, c]), [0], [s])
+    err = normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx))
+    assert err <= TOL[dt], (dt, err)
+
+
 @pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16"])
 def test_conv2d_groups_dilation_flip_strided_output(mx, orc, dt):
     code = getattr(mx, dt)
