@@ -11,6 +11,8 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <unordered_set>
+#include <functional>
 #include <random>
 #include <string>
 #include <vector>
@@ -130,6 +132,25 @@ CASE(grad_graph_structure) {
     EXPECT(g2[0].tape == nullptr && g2[0].shape()[0] == 3, "unused parameter gets zeros");
     EXPECT(throws([&] { (void)matrix::value_and_grad([](std::vector<matrix> p) { return p[0] * 2.0f; })({matrix::leaf({3})}); }),
            "value_and_grad needs a single-element output");
+    // the vjp of Max: one MaxGrad node per operand when the incoming gradient is a contiguous node
+    // output of the broadcast's shape ((y * y).sum() gives 2 y g), the four-node form (with its
+    // Equal) when it is not (the gradient of z.sum(1) is a stride-0 broadcast view)
+    auto has = [](const matrix& m, const char* name) {
+        std::unordered_set<const Primitive*> seen;
+        std::function<bool(const matrix&)> walk = [&](const matrix& n) -> bool {
+            if (!n.tape || !seen.insert(n.tape.get()).second) return false;
+            if (std::string(n.tape->name()) == name) return true;
+            for (uint32_t i = 0; i < n.tape->num_inputs(); i++)
+                if (walk(n.tape->input_at(i))) return true;
+            return false;
+        };
+        return walk(m);
+    };
+    EXPECT(has(g[0], "MaxGrad") && !has(g[0], "Equal"), "dense layer: fused Max backward");
+    matrix z = matrix::max(x, matrix::scalar(0.0f));
+    std::vector<matrix> outs3{z.sum(1).sum()}, p3{x};
+    std::vector<matrix> g3 = matrix::build_grad_graph(outs3, p3);
+    EXPECT(!has(g3[0], "MaxGrad") && has(g3[0], "Equal"), "broadcast gradient: four-node Max backward");
 }
 
 // ------------------------------------------------------------------ GPU cases
