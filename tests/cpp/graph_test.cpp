@@ -593,6 +593,27 @@ CASE(gpu_value_and_grad) {
     std::vector<double> gref(xv.size());
     for (size_t i = 0; i < xv.size(); i++) gref[i] = 6.0 * xv[i];
     EXPECT(rel_err(gv, gref) <= 1e-6, "gradient of 3 x^2");
+    // gradients through Max against a scalar: x.max(0.5).sum(1).sum() takes the four-node vjp (the
+    // gradient reaching the Max is a broadcast view), (m * m).sum() the fused one; ties (x == 0.5)
+    // send the gradient to the scalar, so x gets 0 there
+    auto xv2 = randn(8 * 16, 31);
+    for (size_t i = 0; i < xv2.size(); i += 7) xv2[i] = 0.5f;
+    matrix x2 = matrix::from_host<float>({8, 16}, xv2);
+    auto [v1, g1] = matrix::value_and_grad([](std::vector<matrix> p) {
+        return matrix::max(p[0], matrix::scalar(0.5f)).sum(1).sum();
+    })({x2});
+    auto [v2, g2] = matrix::value_and_grad([](std::vector<matrix> p) {
+        matrix m = matrix::max(p[0], matrix::scalar(0.5f));
+        return (m * m).sum();
+    })({x2});
+    auto g1v = g1[0].to_host<float>();
+    auto g2v = g2[0].to_host<float>();
+    for (size_t i = 0; i < xv2.size(); i++) {
+        const float m = xv2[i] < 0.5f ? 0.5f : xv2[i];
+        const bool to_x = xv2[i] > 0.5f;
+        EXPECT(g1v[i] == (to_x ? 1.0f : 0.0f), "max gradient, four-node form");
+        EXPECT(g2v[i] == (to_x ? 2.0f * m : 0.0f), "max gradient, fused form");
+    }
 }
 
 int main(int argc, char** argv) {
