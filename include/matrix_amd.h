@@ -9,7 +9,8 @@
  *   - nothing throws across it; mx_last_error() gives the message of the last failure on
  *     the calling thread;
  *   - launches are asynchronous on the given stream (NULL = the calling thread's stream,
- *     see mx_hip_stream_for_thread); nothing allocates device memory except mx_hip_alloc;
+ *     see mx_hip_stream_for_thread); nothing allocates device memory except mx_hip_alloc
+ *     (launches take caller workspaces, sized by the *_workspace_bytes queries);
  *   - descriptor arrays (shape / strides) are read on the host during the call and may be
  *     freed as soon as it returns.
  *
@@ -65,6 +66,10 @@ int mx_hip_device_count(int* count);
  * allocation; the host matrix keeps the atomic refcount. */
 int mx_hip_alloc(size_t bytes, void** dptr);
 int mx_hip_free(void* dptr);
+/* Device allocations (mx_hip_alloc) and frees made so far by this process.  No launch entry point
+ * allocates; the counter lets a caller check that a phase such as a graph's execute allocated
+ * nothing (the reference's "no buffer is built during EXECUTE", .agents/MemoryManagement.md:335). */
+int mx_hip_alloc_stats(uint64_t* allocs, uint64_t* frees);
 int mx_hip_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int mx_hip_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int mx_hip_d2d(void* dst, const void* src, size_t bytes, void* stream);
@@ -167,25 +172,42 @@ int mx_launch_max_grad(int op, int side, int dtype, int cdims, const uint32_t* s
  * (Mods/Utils.mm:204-252): shapeC = [batch..., M, N], sA / sBt / sC per axis, whose last
  * entry is the K stride of A and of Bt (the reference requires 1 there; any value is
  * accepted here) and the N stride of C.  float32 runs on fp32 MFMA, float16 / bfloat16 on
- * 16-bit MFMA with fp32 accumulation; integer types accumulate in their own type (wrap). */
+ * 16-bit MFMA with fp32 accumulation; integer types accumulate in their own type (wrap).
+ * This form takes no workspace, so it never splits the K range over blocks (a product with few
+ * output tiles then leaves CUs idle); mx_launch_batched_matmul_ws below does. */
 int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC,
                              const uint32_t* sA, const uint32_t* sBt, const uint32_t* sC,
                              uint32_t K, void* C, const void* A, const void* Bt, void* stream);
+
+/* mx_launch_batched_matmul with a caller workspace, as the reference's primitives allocate
+ * during COMPILE and never during EXECUTE (primitives.cpp:454-470): when the output has too few
+ * tiles to fill the CUs, the K range is split over blocks, the fp32 partials go to the
+ * workspace and a second launch sums them in split order (deterministic).  The size comes from
+ * mx_matmul_workspace_bytes (0: the product never splits, workspace may be NULL); a workspace
+ * smaller than that (or NULL) runs the product unsplit.  Results differ from the unsplit form
+ * only in the fp32 summation order.  Launches sharing a workspace must not overlap in time. */
+int mx_matmul_workspace_bytes(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                              const uint32_t* sBt, const uint32_t* sC, uint32_t K, size_t* bytes);
+int mx_launch_batched_matmul_ws(int dtype, int cdims, const uint32_t* shapeC,
+                                const uint32_t* sA, const uint32_t* sBt, const uint32_t* sC,
+                                uint32_t K, void* C, const void* A, const void* Bt,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* No counterpart in the reference: a Dot node followed by a broadcast Add of a bias row and a
  * Max / Min against a scalar (DotPrimitive, primitives.cpp:5464-5626; AdditionPrimitive,
  * primitives.cpp:397-560; MaxPrimitive / MinPrimitive, primitives.cpp:2515-2824), the bias +
  * ReLU of a dense layer, in one call for a graph compiler that fuses the three nodes.  Computes
- * C as mx_launch_batched_matmul does, then Z = C + bias (bias: N contiguous elements, broadcast
- * over the batch and M) and H = max(Z, s) (act_op MX_OP_MAX) or min(Z, s) (MX_OP_MIN), s one
- * element at act_scalar, each element exactly as mx_launch_bcast_binary computes it, so C, Z
- * and H equal those three launches bit for bit.  float32 / float16 / bfloat16; C, Z and H
- * contiguous with C's shape.  With a split K range the combine launch writes C, Z and H; else
- * one epilogue launch reads C once and writes Z and H. */
+ * C as mx_launch_batched_matmul_ws does (same workspace rules), then Z = C + bias (bias: N
+ * contiguous elements, broadcast over the batch and M) and H = max(Z, s) (act_op MX_OP_MAX) or
+ * min(Z, s) (MX_OP_MIN), s one element at act_scalar, each element exactly as
+ * mx_launch_bcast_binary computes it, so C, Z and H equal those three launches bit for bit.
+ * float32 / float16 / bfloat16; C, Z and H contiguous with C's shape.  With a split K range the
+ * combine launch writes C, Z and H; else one epilogue launch reads C once and writes Z and H. */
 int mx_launch_batched_matmul_bias_act(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
                                       const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
                                       const void* A, const void* Bt, const void* bias, void* Z, int act_op,
-                                      const void* act_scalar, void* H, void* stream);
+                                      const void* act_scalar, void* H, void* workspace,
+                                      size_t workspace_bytes, void* stream);
 
 /* Channels-last N-D convolution, the argument set of conv_gpu (Matrix.mm:12335-12395) /
  * conv2d_gpu (Matrix.mm:5521-5559): input [N, S1..Sn, C], kernel [O, K1..Kn, C/groups],

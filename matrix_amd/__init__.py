@@ -66,6 +66,7 @@ _SIGS = {
     "mx_hip_device_count": ([_ip], _i),
     "mx_hip_alloc": ([_sz, ctypes.POINTER(_vp)], _i),
     "mx_hip_free": ([_vp], _i),
+    "mx_hip_alloc_stats": ([ctypes.POINTER(_u64), ctypes.POINTER(_u64)], _i),
     "mx_hip_h2d": ([_vp, _vp, _sz, _vp], _i),
     "mx_hip_d2h": ([_vp, _vp, _sz, _vp], _i),
     "mx_hip_d2d": ([_vp, _vp, _sz, _vp], _i),
@@ -91,9 +92,11 @@ _SIGS = {
     "mx_broadcast_shapes": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_broadcast_shapes_matmul": ([_u32p, _u32p, _u32, _u32p, _u32p, _u32, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
     "mx_launch_batched_matmul": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp], _i),
+    "mx_matmul_workspace_bytes": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, ctypes.POINTER(_sz)], _i),
+    "mx_launch_batched_matmul_ws": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp, _sz, _vp], _i),
     "mx_launch_max_grad": ([_i, _i, _i, _i, _u32p, _u32p, _u32p, _u32p, _vp, _vp, _vp, _vp, _vp], _i),
     "mx_launch_batched_matmul_bias_act": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32, _vp, _vp, _vp, _vp, _vp, _i,
-                                           _vp, _vp, _vp], _i),
+                                           _vp, _vp, _vp, _sz, _vp], _i),
     "mx_conv_workspace_bytes": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _i, ctypes.POINTER(_sz)], _i),
     "mx_launch_conv_nd": ([_i, _i, _u32p, _u32p, _u32p, _u32p, _u32p, _u32p, _ip, _ip, _ip, _ip,
                            _i, _i, _vp, _vp, _vp, _vp, _sz, _vp], _i),
@@ -318,11 +321,33 @@ def reduce_workspace_bytes(op, dtype, reduce_stride, n_reduce, desc):
     return nb.value
 
 
-def launch_batched_matmul(dtype, desc, K, C, A, Bt, stream=None):
-    """desc = (shapeC [..., M, N], sA, sBt, sC) as collapse_dims_matmul gives it."""
+def matmul_workspace_bytes(dtype, desc, K):
+    """Split-K workspace bytes of a product (mx_matmul_workspace_bytes); 0 when it never splits."""
     shape, sA, sBt, sC = desc
-    check(lib.mx_launch_batched_matmul(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
-                                       int(C), int(A), int(Bt), stream))
+    nb = ctypes.c_size_t()
+    check(lib.mx_matmul_workspace_bytes(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
+                                        ctypes.byref(nb)))
+    return nb.value
+
+
+def launch_batched_matmul(dtype, desc, K, C, A, Bt, stream=None, workspace=0, workspace_bytes=0):
+    """desc = (shapeC [..., M, N], sA, sBt, sC) as collapse_dims_matmul gives it.  With a workspace
+    (mx_launch_batched_matmul_ws) the K range may be split over blocks; without one the
+    reference-signature entry point runs the product unsplit."""
+    shape, sA, sBt, sC = desc
+    if workspace:
+        check(lib.mx_launch_batched_matmul_ws(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
+                                              int(C), int(A), int(Bt), int(workspace), workspace_bytes, stream))
+    else:
+        check(lib.mx_launch_batched_matmul(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
+                                           int(C), int(A), int(Bt), stream))
+
+
+def alloc_stats():
+    """(allocations, frees) of device memory made through the ABI so far."""
+    a, f = ctypes.c_uint64(), ctypes.c_uint64()
+    check(lib.mx_hip_alloc_stats(ctypes.byref(a), ctypes.byref(f)))
+    return a.value, f.value
 
 
 def launch_max_grad(op, side, dtype, desc, R, A, B, G, stream=None):
@@ -333,13 +358,14 @@ def launch_max_grad(op, side, dtype, desc, R, A, B, G, stream=None):
                                  int(B), int(G), stream))
 
 
-def launch_batched_matmul_bias_act(dtype, desc, K, C, A, Bt, bias, Z, act_op, act_scalar, H, stream=None):
+def launch_batched_matmul_bias_act(dtype, desc, K, C, A, Bt, bias, Z, act_op, act_scalar, H, stream=None,
+                                   workspace=0, workspace_bytes=0):
     """C = A . Bt^T, Z = C + bias (N elements), H = act_op(Z, *act_scalar) (OP_MAX / OP_MIN) in one
-    call; desc as for launch_batched_matmul, C / Z / H contiguous."""
+    call; desc and workspace as for launch_batched_matmul, C / Z / H contiguous."""
     shape, sA, sBt, sC = desc
     check(lib.mx_launch_batched_matmul_bias_act(dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K,
                                                 int(C), int(A), int(Bt), int(bias), int(Z), act_op,
-                                                int(act_scalar), int(H), stream))
+                                                int(act_scalar), int(H), int(workspace), workspace_bytes, stream))
 
 
 def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=0, workspace_bytes=0,
@@ -441,14 +467,15 @@ def prepare_reduce(op, dtype, reduce_stride, n_reduce, desc, workspace=0, worksp
     return launch
 
 
-def prepare_batched_matmul(dtype, desc, K, stream=None):
-    """mx_launch_batched_matmul with its descriptor converted once: returns launch(C, A, Bt)."""
+def prepare_batched_matmul(dtype, desc, K, stream=None, workspace=0, workspace_bytes=0):
+    """mx_launch_batched_matmul_ws with its descriptor converted once: returns launch(C, A, Bt)."""
     shape, sA, sBt, sC = desc
-    fn = lib.mx_launch_batched_matmul
+    fn = lib.mx_launch_batched_matmul_ws
     head = (dtype, len(shape), u32(shape), u32(sA), u32(sBt), u32(sC), K)
+    tail = (int(workspace), workspace_bytes, stream)
 
     def launch(C, A, Bt):
-        status = fn(*head, C, A, Bt, stream)
+        status = fn(*head, C, A, Bt, *tail)
         if status != OK:
             raise MatrixAMDError(status, last_error())
 

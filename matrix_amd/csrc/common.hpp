@@ -31,9 +31,6 @@ int hip_fail(hipError_t err, const char* what);
 // set) when the runtime was never initialised.
 bool resolve_stream(void* in, hipStream_t* out);
 
-// A device buffer of at least `bytes` owned by the library for work on stream `st` (reused by
-// every launch on that stream; growing it synchronises the stream).
-int stream_scratch(hipStream_t st, size_t bytes, void** out);
 
 // ------------------------------------------------------------------ element types
 struct half_bits { uint16_t v; };   // IEEE binary16, stored raw

@@ -376,8 +376,27 @@ uint32_t choose_split(const tile::TileShape& ts, const GemmArgs& g, uint32_t pai
     return (g.K + *ksplit - 1) / *ksplit;
 }
 
+// Bytes of fp32 partials a split K range of this product needs ([split][batch][M][N]), 0 when the
+// tile kernel would not split it or the skinny kernel takes it with 16-byte aligned operands.  (A
+// skinny-shaped product with misaligned operands goes to the tile kernel, and runs unsplit when
+// the workspace sized here is 0.)
 template <int DT>
-int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st, const Epi* epi = nullptr) {
+size_t split_bytes(const GemmArgs& g) {
+    using S = typename MmaTraits<DT>::S;
+    alignas(16) static const char aligned[16] = {};
+    if (skinny_ok<DT>(g, aligned, aligned)) return 0;
+    const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
+    uint32_t ksplit = 0;
+    const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
+    const uint64_t per = (uint64_t)g.batches * g.M * g.N;
+    return nsplit > 1 && per < 0xffffffffull ? (size_t)nsplit * per * sizeof(float) : 0;
+}
+
+// ws / ws_bytes: the caller's workspace for split-K partials.  A product whose split needs more
+// than ws_bytes (none given: 0) runs unsplit; nothing here allocates.
+template <int DT>
+int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, size_t ws_bytes, hipStream_t st,
+                const Epi* epi = nullptr) {
     using S = typename MmaTraits<DT>::S;
     constexpr int CE = 16 / sizeof(S);
     if (skinny_ok<DT>(g, A, Bt)) {
@@ -386,8 +405,9 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t
     }
     const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
     uint32_t ksplit = 0;
-    const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
+    uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
     const uint64_t per = (uint64_t)g.batches * g.M * g.N;
+    if (nsplit > 1 && (ws == nullptr || (size_t)nsplit * per * sizeof(float) > ws_bytes)) nsplit = 1;
     // the DMA path addresses a tile's rows with 32-bit byte offsets
     const bool vec = g.ka == 1 && g.kb == 1 && g.lda % CE == 0 && g.ldb % CE == 0 &&
                      (uint64_t)ts.bm * g.lda * sizeof(S) < (1ull << 32) &&
@@ -411,10 +431,9 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t
     const tile::MatrixSrc::Geom geo{};
     const char* who = "mx_launch_batched_matmul";
     if (nsplit > 1 && per < 0xffffffffull) {
-        // fp32 partials [split][batch][M][N] in the stream's scratch, then an ordered sum
-        void* P = nullptr;
-        int rc = stream_scratch(st, (size_t)nsplit * per * sizeof(float), &P);
-        if (rc) return rc;
+        // fp32 partials [split][batch][M][N] in the caller's workspace, then an ordered sum
+        void* P = ws;
+        int rc = MX_OK;
         GemmArgs gp = g;
         gp.ksplit = ksplit;
         gp.ldc = g.N;
@@ -505,18 +524,14 @@ int matmul_args(const char* who, int cdims, const uint32_t* shapeC, const uint32
 
 }  // namespace
 
-extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
-                                        const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
-                                        const void* A, const void* Bt, void* stream) {
-    GemmArgs g;
-    const int ar = matmul_args("mx_launch_batched_matmul", cdims, shapeC, sA, sBt, sC, K, C, A, Bt, g);
-    if (ar) return ar < 0 ? MX_OK : ar;
-    hipStream_t st;
-    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+namespace {
+
+int launch_any(int dtype, GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, size_t ws_bytes,
+               hipStream_t st) {
     switch (dtype) {
-    case MX_FLOAT32: return launch_mfma<MX_FLOAT32>(g, C, A, Bt, st);
-    case MX_FLOAT16: return launch_mfma<MX_FLOAT16>(g, C, A, Bt, st);
-    case MX_BFLOAT16: return launch_mfma<MX_BFLOAT16>(g, C, A, Bt, st);
+    case MX_FLOAT32: return launch_mfma<MX_FLOAT32>(g, C, A, Bt, ws, ws_bytes, st);
+    case MX_FLOAT16: return launch_mfma<MX_FLOAT16>(g, C, A, Bt, ws, ws_bytes, st);
+    case MX_BFLOAT16: return launch_mfma<MX_BFLOAT16>(g, C, A, Bt, ws, ws_bytes, st);
     case MX_INT32: return launch_scalar<MX_INT32>(g, C, A, Bt, st);
     case MX_INT16: return launch_scalar<MX_INT16>(g, C, A, Bt, st);
     case MX_INT8: return launch_scalar<MX_INT8>(g, C, A, Bt, st);
@@ -531,10 +546,52 @@ extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* sh
     }
 }
 
+}  // namespace
+
+extern "C" int mx_matmul_workspace_bytes(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                         const uint32_t* sBt, const uint32_t* sC, uint32_t K, size_t* bytes) {
+    if (!bytes) return fail(MX_ERR_INVALID_ARG, "mx_matmul_workspace_bytes: null out pointer");
+    *bytes = 0;
+    GemmArgs g;
+    // buffers are not needed to size the workspace: pass a placeholder so the null check passes
+    static const char dummy[16] = {};
+    const int ar = matmul_args("mx_matmul_workspace_bytes", cdims, shapeC, sA, sBt, sC, K, (void*)dummy, dummy,
+                               dummy, g);
+    if (ar) return ar < 0 ? MX_OK : ar;
+    switch (dtype) {
+    case MX_FLOAT32: *bytes = split_bytes<MX_FLOAT32>(g); return MX_OK;
+    case MX_FLOAT16: *bytes = split_bytes<MX_FLOAT16>(g); return MX_OK;
+    case MX_BFLOAT16: *bytes = split_bytes<MX_BFLOAT16>(g); return MX_OK;
+    case MX_INT32: case MX_INT16: case MX_INT8: case MX_INT64: case MX_UINT8: case MX_UINT16: case MX_UINT32:
+    case MX_UINT64: case MX_BOOL: return MX_OK;
+    default:
+        return fail(MX_ERR_UNSUPPORTED, "mx_matmul_workspace_bytes: no kernel for dtype " + std::to_string(dtype));
+    }
+}
+
+extern "C" int mx_launch_batched_matmul_ws(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                           const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
+                                           const void* A, const void* Bt, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+    GemmArgs g;
+    const int ar = matmul_args("mx_launch_batched_matmul", cdims, shapeC, sA, sBt, sC, K, C, A, Bt, g);
+    if (ar) return ar < 0 ? MX_OK : ar;
+    hipStream_t st;
+    if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+    return launch_any(dtype, g, C, A, Bt, workspace, workspace ? workspace_bytes : 0, st);
+}
+
+extern "C" int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
+                                        const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
+                                        const void* A, const void* Bt, void* stream) {
+    return mx_launch_batched_matmul_ws(dtype, cdims, shapeC, sA, sBt, sC, K, C, A, Bt, nullptr, 0, stream);
+}
+
 extern "C" int mx_launch_batched_matmul_bias_act(int dtype, int cdims, const uint32_t* shapeC, const uint32_t* sA,
                                                  const uint32_t* sBt, const uint32_t* sC, uint32_t K, void* C,
                                                  const void* A, const void* Bt, const void* bias, void* Z,
-                                                 int act_op, const void* act_scalar, void* H, void* stream) {
+                                                 int act_op, const void* act_scalar, void* H, void* workspace,
+                                                 size_t workspace_bytes, void* stream) {
     const char* who = "mx_launch_batched_matmul_bias_act";
     if (dtype != MX_FLOAT32 && dtype != MX_FLOAT16 && dtype != MX_BFLOAT16)
         return fail(MX_ERR_UNSUPPORTED, std::string(who) + ": float32 / float16 / bfloat16 only, dtype " +
@@ -556,9 +613,10 @@ extern "C" int mx_launch_batched_matmul_bias_act(int dtype, int cdims, const uin
     hipStream_t st;
     if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
     const Epi e{Z, H, bias, act_scalar, act_op};
+    const size_t wsb = workspace ? workspace_bytes : 0;
     switch (dtype) {
-    case MX_FLOAT32: return launch_mfma<MX_FLOAT32>(g, C, A, Bt, st, &e);
-    case MX_FLOAT16: return launch_mfma<MX_FLOAT16>(g, C, A, Bt, st, &e);
-    default: return launch_mfma<MX_BFLOAT16>(g, C, A, Bt, st, &e);
+    case MX_FLOAT32: return launch_mfma<MX_FLOAT32>(g, C, A, Bt, workspace, wsb, st, &e);
+    case MX_FLOAT16: return launch_mfma<MX_FLOAT16>(g, C, A, Bt, workspace, wsb, st, &e);
+    default: return launch_mfma<MX_BFLOAT16>(g, C, A, Bt, workspace, wsb, st, &e);
     }
 }

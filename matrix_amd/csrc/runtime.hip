@@ -53,39 +53,12 @@ bool resolve_stream(void* in, hipStream_t* out) {
     return thread_stream(out) == MX_OK;
 }
 
-// Library-owned scratch, one buffer per stream: work queued on one stream runs in order, so
-// every launch on that stream may reuse the buffer.  Growing it waits for the stream (the old
-// buffer may still be in use by queued work) and then reallocates.
+// Device allocations made through the ABI (mx_hip_alloc) and frees, counted so a caller can
+// check that a phase allocated nothing (the reference's "no buffer is built during EXECUTE",
+// .agents/MemoryManagement.md:335).  No kernel entry point allocates.
 namespace {
-struct Scratch { void* ptr = nullptr; size_t bytes = 0; };
-std::mutex g_scratch_mu;
-std::unordered_map<hipStream_t, Scratch> g_scratch;
+std::atomic<uint64_t> g_allocs{0}, g_frees{0};
 }  // namespace
-
-int stream_scratch(hipStream_t st, size_t bytes, void** out) {
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    Scratch& s = g_scratch[st];
-    if (s.bytes < bytes) {
-        const size_t want = bytes < (size_t)1 << 20 ? (size_t)1 << 20 : bytes + bytes / 4;
-        if (s.ptr) {
-            MX_HIP(hipStreamSynchronize(st));
-            MX_HIP(hipFree(s.ptr));
-            s.ptr = nullptr;
-            s.bytes = 0;
-        }
-        MX_HIP(hipMalloc(&s.ptr, want));
-        s.bytes = want;
-    }
-    *out = s.ptr;
-    return MX_OK;
-}
-
-static void release_scratch() {
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    for (auto& kv : g_scratch)
-        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
-    g_scratch.clear();
-}
 
 }  // namespace mx
 
@@ -128,7 +101,6 @@ int mx_hip_shutdown(void) {
         (void)hipStreamDestroy(kv.second);
     }
     g_streams.clear();
-    release_scratch();
     g_device.store(-1);
     return rc;
 }
@@ -139,12 +111,21 @@ int mx_hip_alloc(size_t bytes, void** dptr) {
     *dptr = nullptr;
     if (bytes == 0) return MX_OK;
     MX_HIP(hipMalloc(dptr, bytes));
+    g_allocs.fetch_add(1, std::memory_order_relaxed);
     return MX_OK;
 }
 
 int mx_hip_free(void* dptr) {
     if (!dptr) return MX_OK;
     MX_HIP(hipFree(dptr));
+    g_frees.fetch_add(1, std::memory_order_relaxed);
+    return MX_OK;
+}
+
+int mx_hip_alloc_stats(uint64_t* allocs, uint64_t* frees) {
+    if (!allocs || !frees) return fail(MX_ERR_INVALID_ARG, "mx_hip_alloc_stats: null pointer");
+    *allocs = g_allocs.load(std::memory_order_relaxed);
+    *frees = g_frees.load(std::memory_order_relaxed);
     return MX_OK;
 }
 
@@ -200,17 +181,7 @@ int mx_hip_stream_create(void** stream) {
 
 int mx_hip_stream_destroy(void* stream) {
     if (!stream) return MX_OK;
-    hipStream_t s = (hipStream_t)stream;
-    {
-        std::lock_guard<std::mutex> lk(g_scratch_mu);     // the stream's split-K scratch, if any
-        auto it = g_scratch.find(s);
-        if (it != g_scratch.end()) {
-            MX_HIP(hipStreamSynchronize(s));
-            if (it->second.ptr) MX_HIP(hipFree(it->second.ptr));
-            g_scratch.erase(it);
-        }
-    }
-    MX_HIP(hipStreamDestroy(s));
+    MX_HIP(hipStreamDestroy((hipStream_t)stream));
     return MX_OK;
 }
 

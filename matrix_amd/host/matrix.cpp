@@ -127,6 +127,21 @@ const char* dtype_name(dtype t) {
     return i < 13 ? names[i] : "?";
 }
 
+dtype promote_types(dtype a, dtype b) {
+    if (a == b) return a;
+    if (a == dtype::Complex64 || b == dtype::Complex64) return dtype::Complex64;
+    if (a == dtype::Bool) return b;
+    if (b == dtype::Bool) return a;
+    if (is_floating(a) || is_floating(b)) return dtype::Float;     // Float, or a 16-bit float with another type
+    const int wa = (int)dtype_size(a) * 8, wb = (int)dtype_size(b) * 8;
+    if (is_unsigned(a) == is_unsigned(b)) return wa >= wb ? a : b;
+    const dtype s = is_unsigned(a) ? b : a;                        // the signed one
+    const int ws = is_unsigned(a) ? wb : wa, wu = is_unsigned(a) ? wa : wb;
+    if (wu < ws) return s;
+    if (wu == 64) return dtype::Float;
+    return wu == 8 ? dtype::Int16 : dtype::Int32;
+}
+
 namespace matrix_amd {
 namespace {
 std::once_flag g_init_once;
@@ -192,7 +207,6 @@ matrix matrix::full(const std::vector<size_m>& shape, double value, dtype type) 
     return m;
 }
 
-matrix matrix::scalar(double value, dtype type) { return full({}, value, type); }
 
 void* matrix::host_data() {
     if (tape || !storage || !storage->host_is_source) throw std::logic_error("matrix::host_data: not a leaf");
@@ -388,7 +402,7 @@ struct BinaryPrim : Primitive {
         case MX_OP_MUL: return {(g * b).unbroadcast_shape(as, a.dims), (g * a).unbroadcast_shape(bs, b.dims)};
         case MX_OP_DIV: {
             matrix ga = g / b;
-            matrix gb = (g * a) / (b * b) * -1.0f;
+            matrix gb = g * matrix::scalar(-1, a.type) * a / (b * b);
             return {ga.unbroadcast_shape(as, a.dims), gb.unbroadcast_shape(bs, b.dims)};
         }
         case MX_OP_MAX:
@@ -477,6 +491,7 @@ struct DotPrim : Primitive {
     uint32_t cd = 0, K = 0;
     uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sC[MX_MAX_DIMS];
     std::shared_ptr<DotEpilogue> epi;
+    DevBuf ws;                      // split-K partials, reserved at compile
     DotPrim(matrix x, matrix y) : a(std::move(x)), bt(std::move(y)) {}
     const char* name() const override { return "Dot"; }
     uint32_t num_inputs() const override { return 2; }
@@ -492,6 +507,9 @@ struct DotPrim : Primitive {
         } else {
             check(mx_collapse_dims_matmul(os, b1t, b2t, ost, out.dims, kCap, cs, sA, sB, sC, &cd), "collapse_dims_matmul");
         }
+        size_t bytes = 0;
+        check(mx_matmul_workspace_bytes((int)a.type, (int)cd, cs, sA, sB, sC, K, &bytes), "matmul workspace");
+        if (bytes) ws.reserve(bytes);
     }
     void execute(const matrix& out) override {
         if (epi) {
@@ -501,13 +519,14 @@ struct DotPrim : Primitive {
             if (z && h && z->dev && h->dev && bs->dev && !bs->dev_stale && ss->dev && !ss->dev_stale) {
                 check(mx_launch_batched_matmul_bias_act((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a),
                                                         dptr(bt), dptr(epi->bias), z->dev, epi->act, dptr(epi->s),
-                                                        h->dev, stream),
+                                                        h->dev, ws.p, ws.bytes, stream),
                       "launch Dot + bias + activation");
                 epi->gen = t_exec_gen;
                 return;
             }
         }
-        check(mx_launch_batched_matmul((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a), dptr(bt), stream),
+        check(mx_launch_batched_matmul_ws((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a), dptr(bt), ws.p,
+                                          ws.bytes, stream),
               "launch Dot");
     }
     std::vector<matrix> vjp(matrix& g) override {
@@ -604,31 +623,10 @@ struct ConvPrim : Primitive {
     std::vector<matrix> vjp(matrix&) override { throw std::logic_error("matrix: no vjp for Convolve"); }
 };
 
-// Result dtype of a binary op: equal dtypes pass; a rank-0 operand takes the other's dtype
-// (scalar_operand_type); otherwise the wider of the two, floats before integers.
-dtype common_type(const matrix& a, const matrix& b) {
-    if (a.type == b.type) return a.type;
-    if (a.dims == 0 && b.dims > 0) return b.type;
-    if (b.dims == 0 && a.dims > 0) return a.type;
-    auto rank = [](dtype t) {
-        switch (t) {
-        case dtype::Float: return 100;
-        case dtype::BFloat16: return 91;
-        case dtype::Float16: return 90;
-        case dtype::Int64: case dtype::UInt64: return 60;
-        case dtype::Int32: case dtype::UInt32: return 50;
-        case dtype::Int16: case dtype::UInt16: return 40;
-        default: return 30;
-        }
-    };
-    if ((a.type == dtype::Float16 && b.type == dtype::BFloat16) || (a.type == dtype::BFloat16 && b.type == dtype::Float16))
-        return dtype::Float;
-    return rank(a.type) >= rank(b.type) ? a.type : b.type;
-}
-
+// The operands are cast to their promoted dtype first, as operator+ does (Matrix.mm:8312-8315).
 matrix binary(int op, const matrix& x, const matrix& y) {
     if (!x.storage || !y.storage) throw std::invalid_argument("matrix: operand is empty");
-    const dtype t = common_type(x, y);
+    const dtype t = promote_types(x.type, y.type);
     matrix a = x.type == t ? x : x.astype(t);
     matrix b = y.type == t ? y : y.astype(t);
     uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
@@ -722,14 +720,11 @@ matrix operator-(const matrix& a, const matrix& b) { return binary(MX_OP_SUB, a,
 matrix operator*(const matrix& a, const matrix& b) { return binary(MX_OP_MUL, a, b); }
 matrix operator/(const matrix& a, const matrix& b) { return binary(MX_OP_DIV, a, b); }
 
-// max / min do not cast (Matrix.mm:13363-13376): the operands must share a dtype, except a
-// rank-0 scalar, which takes the other operand's.
-static void require_same_type(const matrix& a, const matrix& b, const char* who) {
-    if (a.type != b.type && a.dims != 0 && b.dims != 0)
-        throw std::invalid_argument(std::string("matrix::") + who + ": operands must have the same dtype");
-}
-matrix matrix::max(const matrix& a, const matrix& b) { require_same_type(a, b, "max"); return binary(MX_OP_MAX, a, b); }
-matrix matrix::min(const matrix& a, const matrix& b) { require_same_type(a, b, "min"); return binary(MX_OP_MIN, a, b); }
+// max / min give the promoted dtype (Matrix.mm:13363-13376).  The reference leaves operands of
+// another dtype uncast, so its kernel then reads them in the result's dtype; here they are cast
+// first, which gives the same values whenever the operands already share the result's dtype.
+matrix matrix::max(const matrix& a, const matrix& b) { return binary(MX_OP_MAX, a, b); }
+matrix matrix::min(const matrix& a, const matrix& b) { return binary(MX_OP_MIN, a, b); }
 matrix matrix::equal(const matrix& a, const matrix& b) { return binary(MX_OP_EQ, a, b); }
 
 matrix matrix::sum(int axis, bool keepdims) const { return reduce(MX_RED_SUM, *this, axis, keepdims, "sum"); }

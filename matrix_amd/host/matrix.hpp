@@ -37,6 +37,21 @@ using size_m = uint32_t;
 size_t dtype_size(dtype t);
 const char* dtype_name(dtype t);
 
+constexpr bool is_complex(dtype d) { return d == dtype::Complex64; }
+constexpr bool is_floating(dtype d) { return d == dtype::Float || d == dtype::Float16 || d == dtype::BFloat16; }
+constexpr bool is_integral(dtype d) { return !is_floating(d) && !is_complex(d) && d != dtype::Bool; }
+constexpr bool is_unsigned(dtype d) {
+    return d == dtype::UInt8 || d == dtype::UInt16 || d == dtype::UInt32 || d == dtype::UInt64;
+}
+
+// The dtype of a binary op's result (type_rules / promote_types, matrix.h:166-180,
+// Matrix.mm:107-109): Complex64 absorbs everything; Bool takes the other dtype; Float absorbs
+// the rest; a 16-bit float with anything but itself or Bool is Float; two integers of one
+// signedness take the wider; a signed and an unsigned integer take the signed one when it is
+// wider, else Float next to UInt64, else the signed type twice the unsigned's width (at most
+// Int32).
+dtype promote_types(dtype a, dtype b);
+
 template <typename T> constexpr dtype dtype_of() {
     if constexpr (std::is_same_v<T, float>) return dtype::Float;
     else if constexpr (std::is_same_v<T, int32_t>) return dtype::Int32;
@@ -102,7 +117,14 @@ public:
         if (dtype_size(type) != sizeof(T)) throw std::invalid_argument("matrix::from_host: element size mismatch");
         return from_bytes(shape, type, data.data());
     }
-    static matrix scalar(double value, dtype type = dtype::Float);
+    // A rank-0 matrix holding val converted to type (matrix.h:648-660: static_cast, the 16-bit
+    // floats rounded to nearest even).
+    template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
+    static matrix scalar(T val, dtype type = dtype_of<T>()) {
+        matrix m = leaf({}, type);
+        store_scalar(type, val, m.host_data());
+        return m;
+    }
     static matrix full(const std::vector<size_m>& shape, double value, dtype type = dtype::Float);
     static matrix zeros(const std::vector<size_m>& shape, dtype type = dtype::Float) { return full(shape, 0.0, type); }
     static matrix ones(const std::vector<size_m>& shape, dtype type = dtype::Float) { return full(shape, 1.0, type); }
@@ -185,23 +207,97 @@ public:
 private:
     std::vector<size_m> shp_, str_;
     friend class Primitive;
+    template <typename T> static void store_scalar(dtype type, T val, void* dst);
 };
 
-// Scalars on either side take the matrix's dtype (scalar_operand_type, matrix.h:494).
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator+(const matrix& a, T v) { return a + matrix::scalar((double)v, a.type); }
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator+(T v, const matrix& a) { return matrix::scalar((double)v, a.type) + a; }
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator-(const matrix& a, T v) { return a - matrix::scalar((double)v, a.type); }
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator-(T v, const matrix& a) { return matrix::scalar((double)v, a.type) - a; }
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator*(const matrix& a, T v) { return a * matrix::scalar((double)v, a.type); }
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator*(T v, const matrix& a) { return matrix::scalar((double)v, a.type) * a; }
-template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
-inline matrix operator/(const matrix& a, T v) { return a / matrix::scalar((double)v, a.type); }
+template <typename T>
+void matrix::store_scalar(dtype type, T v, void* dst) {
+    auto put = [dst](auto x) { std::memcpy(dst, &x, sizeof(x)); };
+    switch (type) {
+    case dtype::Float: put(static_cast<float>(v)); break;
+    case dtype::Float16: put(static_cast<_Float16>(v)); break;
+    case dtype::BFloat16: put(static_cast<__bf16>(static_cast<float>(v))); break;
+    case dtype::Int8: put(static_cast<int8_t>(v)); break;
+    case dtype::UInt8: put(static_cast<uint8_t>(v)); break;
+    case dtype::Bool: put(static_cast<uint8_t>(v != T(0))); break;
+    case dtype::Int16: put(static_cast<int16_t>(v)); break;
+    case dtype::UInt16: put(static_cast<uint16_t>(v)); break;
+    case dtype::Int32: put(static_cast<int32_t>(v)); break;
+    case dtype::UInt32: put(static_cast<uint32_t>(v)); break;
+    case dtype::Int64: put(static_cast<int64_t>(v)); break;
+    case dtype::UInt64: put(static_cast<uint64_t>(v)); break;
+    case dtype::Complex64: { float c[2] = {static_cast<float>(v), 0.0f}; std::memcpy(dst, c, 8); break; }
+    }
+}
+
+// The dtype a C++ scalar takes next to a matrix of dtype m (scalar_operand_type,
+// matrix.h:1815-1840): m itself whenever that holds the value, so the scalar never widens the
+// matrix (uint8 * 2 stays uint8, half * 0.5f stays Float16), otherwise the narrowest dtype that
+// does and that promote_types then settles on:
+//   - m Float / BFloat16 / Complex64, or a bool scalar: m;
+//   - m Float16: m within +-65504, else Float;
+//   - a floating-point scalar next to an integer (or Bool) matrix: Float;
+//   - an integer scalar: m if it fits, else Int32, else UInt32 (m unsigned), else Int64
+//     (m not UInt64), else UInt64 (m unsigned); std::overflow_error when none holds it.
+namespace matrix_amd_detail {
+template <typename T>
+constexpr bool in_range(T v, long double lo, long double hi) {
+    if constexpr (std::is_floating_point_v<T>) return v >= (T)lo && v <= (T)hi;
+    else if constexpr (std::is_signed_v<T>) return (long double)v >= lo && (long double)v <= hi;
+    else return (long double)v <= hi;
+}
+}  // namespace matrix_amd_detail
+
+template <typename T>
+dtype scalar_operand_type(T v, dtype m) {
+    static_assert(std::is_arithmetic_v<T>, "matrix op with a non-arithmetic scalar");
+    using matrix_amd_detail::in_range;
+    if (m == dtype::Float || m == dtype::BFloat16 || m == dtype::Complex64) return m;
+    if constexpr (std::is_same_v<T, bool>) return m;
+    if (m == dtype::Float16) return in_range(v, -65504.0L, 65504.0L) ? m : dtype::Float;
+    if constexpr (std::is_floating_point_v<T>) {
+        return dtype::Float;
+    } else {
+        auto holds = [&](dtype d) -> bool {
+            switch (d) {
+            case dtype::Int8: return in_range(v, -128.0L, 127.0L);
+            case dtype::UInt8: return in_range(v, 0.0L, 255.0L);
+            case dtype::Int16: return in_range(v, -32768.0L, 32767.0L);
+            case dtype::UInt16: return in_range(v, 0.0L, 65535.0L);
+            case dtype::Int32: return in_range(v, -2147483648.0L, 2147483647.0L);
+            case dtype::UInt32: return in_range(v, 0.0L, 4294967295.0L);
+            case dtype::Int64: return in_range(v, -9223372036854775808.0L, 9223372036854775807.0L);
+            case dtype::UInt64: if constexpr (std::is_signed_v<T>) return v >= 0; else return true;
+            default: return false;
+            }
+        };
+        if (holds(m)) return m;                  // Bool holds no integer scalar: Int32 next
+        if (holds(dtype::Int32)) return dtype::Int32;
+        const bool mu = is_unsigned(m);
+        if (mu && holds(dtype::UInt32)) return dtype::UInt32;
+        if (m != dtype::UInt64 && holds(dtype::Int64)) return dtype::Int64;
+        if (mu && holds(dtype::UInt64)) return dtype::UInt64;
+        throw std::overflow_error("matrix op: scalar " + std::to_string(v) +
+                                  " doesn't fit any dtype it could promote to");
+    }
+}
+
+// matrix (op) scalar and scalar (op) matrix: the scalar becomes a rank-0 matrix of
+// scalar_operand_type(scalar, m.type) and the matrix operator promotes (matrix.h:1842-1870).
+#define MATRIX_AMD_SCALAR_OP(OP)                                                              \
+    template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>              \
+    inline matrix operator OP(const matrix& m, T v) {                                        \
+        return m OP matrix::scalar(v, scalar_operand_type(v, m.type));                       \
+    }                                                                                         \
+    template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>              \
+    inline matrix operator OP(T v, const matrix& m) {                                        \
+        return matrix::scalar(v, scalar_operand_type(v, m.type)) OP m;                       \
+    }
+MATRIX_AMD_SCALAR_OP(+)
+MATRIX_AMD_SCALAR_OP(-)
+MATRIX_AMD_SCALAR_OP(*)
+MATRIX_AMD_SCALAR_OP(/)
+#undef MATRIX_AMD_SCALAR_OP
 
 // A node of the graph: the reference's Primitive contract (primitives.cpp:57-118).  compile()
 // prepares descriptors and workspace once; execute() only launches; vjp() builds the gradient

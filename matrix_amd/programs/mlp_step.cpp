@@ -7,12 +7,16 @@
 // compile_metal / execute_metal does (Matrix.mm:8452-8475).  Inputs ~ N(0,1), weights
 // ~ N(0, 1/fan_in), biases zero, targets ~ U(0,1), all seeded.
 //
-//   mlp_step [--steps K] [--warmup W] [--batch B]
+//   mlp_step [--steps K] [--warmup W] [--batch B] [--dump DIR]
 // prints one JSON line: ms per step (wall clock around the timed steps, each step ending in
-// the stream wait of execute), steps/s and the step's algorithmic TFLOP/s.
+// the stream wait of execute), steps/s, the step's algorithmic TFLOP/s and the device
+// allocations made during all the executes (0: compile allocated everything).  --dump writes the
+// inputs, parameters, pre-activations, loss and gradients of the last step as raw float32 into DIR.
 #include "../host/matrix.hpp"
+#include "../../include/matrix_amd.h"
 
 #include <chrono>
+#include <fstream>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -32,10 +36,12 @@ static std::vector<float> normal(size_t n, uint64_t seed, float stddev) {
 int main(int argc, char** argv) {
     int steps = 100, warmup = 5;
     size_m B = 512;
+    std::string dump;
     for (int i = 1; i + 1 < argc; i += 2) {
         if (!std::strcmp(argv[i], "--steps")) steps = std::atoi(argv[i + 1]);
         else if (!std::strcmp(argv[i], "--warmup")) warmup = std::atoi(argv[i + 1]);
         else if (!std::strcmp(argv[i], "--batch")) B = (size_m)std::atoi(argv[i + 1]);
+        else if (!std::strcmp(argv[i], "--dump")) dump = argv[i + 1];
     }
     const size_m D[4] = {1024, 4096, 4096, 10};
     try {
@@ -54,8 +60,10 @@ int main(int argc, char** argv) {
             params.push_back(matrix::zeros({D[l + 1]}));
         }
         matrix h = x;
+        std::vector<matrix> zs;            // pre-activations, for --dump
         for (int l = 0; l < 3; l++) {
             matrix z = h.dot(params[2 * l]) + params[2 * l + 1];
+            zs.push_back(z);
             h = l < 2 ? matrix::max(z, matrix::scalar(0.0f)) : z;
         }
         matrix d = h - t;
@@ -68,6 +76,8 @@ int main(int argc, char** argv) {
         auto t0 = std::chrono::steady_clock::now();
         matrix::compile_gpu(all);
         auto t1 = std::chrono::steady_clock::now();
+        uint64_t a0 = 0, f0 = 0, a1 = 0, f1 = 0;
+        if (mx_hip_alloc_stats(&a0, &f0) != MX_OK) throw std::runtime_error(mx_last_error());
         for (int i = 0; i < warmup; i++) {
             matrix::execute_gpu(all);
             matrix::clear_trace_checks(all);
@@ -78,6 +88,26 @@ int main(int argc, char** argv) {
             matrix::clear_trace_checks(all);
         }
         auto t3 = std::chrono::steady_clock::now();
+        if (mx_hip_alloc_stats(&a1, &f1) != MX_OK) throw std::runtime_error(mx_last_error());
+        if (!dump.empty()) {
+            matrix::execute_gpu(all);      // one more step, whose values stay evaluated
+            auto put = [&](const std::string& name, const matrix& m) {
+                const std::vector<uint8_t> b = m.to_host_bytes();
+                std::ofstream f(dump + "/" + name + ".bin", std::ios::binary);
+                f.write(reinterpret_cast<const char*>(b.data()), (std::streamsize)b.size());
+                if (!f) throw std::runtime_error("mlp_step: cannot write " + dump + "/" + name + ".bin");
+            };
+            put("x", x);
+            put("t", t);
+            for (int l = 0; l < 3; l++) {
+                put("W" + std::to_string(l), params[2 * l]);
+                put("b" + std::to_string(l), params[2 * l + 1]);
+                put("gW" + std::to_string(l), grads[2 * l]);
+                put("gb" + std::to_string(l), grads[2 * l + 1]);
+                put("z" + std::to_string(l), zs[l]);
+            }
+            put("loss", loss);
+        }
         const double ms = std::chrono::duration<double, std::milli>(t3 - t2).count() / (steps > 0 ? steps : 1);
         const double compile_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
         // forward 2 B (D0 D1 + D1 D2 + D2 D3); backward twice that, less the input gradient of layer 1
@@ -87,8 +117,9 @@ int main(int argc, char** argv) {
         const float lv = loss.to_host<float>()[0];
         std::printf("{\"workload\": \"mlp_step\", \"batch\": %u, \"steps\": %d, \"warmup\": %d, \"ms_per_step\": %.4f, "
                     "\"steps_per_s\": %.3f, \"tflops\": %.3f, \"flop_per_step\": %.0f, \"compile_ms\": %.2f, "
-                    "\"loss\": %.6e}\n",
-                    B, steps, warmup, ms, 1000.0 / ms, flop / (ms * 1e-3) / 1e12, flop, compile_ms, (double)lv);
+                    "\"loss\": %.6e, \"allocs_during_execute\": %llu, \"frees_during_execute\": %llu}\n",
+                    B, steps, warmup, ms, 1000.0 / ms, flop / (ms * 1e-3) / 1e12, flop, compile_ms, (double)lv,
+                    (unsigned long long)(a1 - a0), (unsigned long long)(f1 - f0));
     } catch (const std::exception& e) {
         std::fprintf(stderr, "mlp_step: %s\n", e.what());
         return 1;

@@ -7,6 +7,7 @@
 //
 // Prints "PASS <name>" / "FAIL <name>: <why>" per case; exit status 1 if any case failed.
 #include "../../matrix_amd/host/matrix.hpp"
+#include "../../include/matrix_amd.h"
 
 #include <cmath>
 #include <cstdio>
@@ -559,8 +560,11 @@ CASE(gpu_mlp_training_step_compile_once) {
     std::vector<matrix> all = grads;
     all.push_back(loss);
     matrix::compile_gpu(all);
-    // executes 0 (eager), 1 (captured into a HIP graph), 2-4 (replays of it); new inputs through
-    // the compiled graph before executes 2 and 4: host write + mark_changed
+    // five executes of the compiled graph; new inputs before executes 2 and 4 (host write +
+    // mark_changed); no execute allocates device memory (an execute may free: the executor's
+    // cache of recent schedules drops the oldest, and with it the earlier cases' graphs)
+    uint64_t a0 = 0, f0 = 0, a1 = 0, f1 = 0;
+    EXPECT(mx_hip_alloc_stats(&a0, &f0) == MX_OK, "alloc stats");
     for (int iter = 0; iter < 5; iter++) {
         if (iter == 2 || iter == 4) {
             auto x2 = randn((size_t)s.B * s.D0, 99 + iter);
@@ -569,6 +573,9 @@ CASE(gpu_mlp_training_step_compile_once) {
             xv = x2;
         }
         matrix::execute_gpu(all);
+        EXPECT(mx_hip_alloc_stats(&a1, &f1) == MX_OK && a1 == a0,
+               "execute " + std::to_string(iter) + " allocated device memory: " + std::to_string(a1 - a0) +
+                   " allocations");
         double lref;
         std::vector<std::vector<double>> dW, db;
         host_mlp(s, xv, tv, Wv, bv, lref, dW, db);
@@ -578,6 +585,9 @@ CASE(gpu_mlp_training_step_compile_once) {
             EXPECT(rel_err(grads[2 * l].to_host<float>(), dW[l]) <= 1e-4, "dW mismatch, layer " + std::to_string(l));
             EXPECT(rel_err(grads[2 * l + 1].to_host<float>(), db[l]) <= 1e-4, "db mismatch, layer " + std::to_string(l));
         }
+        EXPECT(mx_hip_alloc_stats(&a1, &f1) == MX_OK && a1 == a0,
+               "reading the results of execute " + std::to_string(iter) + " allocated device memory: " +
+                   std::to_string(a1 - a0) + " allocations");
         matrix::clear_trace_checks(all);
     }
 }

@@ -27,7 +27,9 @@ def matmul_desc(mx, a_shape, a_strides, bt_shape, bt_strides):
 
 
 def run_mm(mx, orc, code, a, bt, a_shape=None, a_strides=None, bt_shape=None, bt_strides=None, acc=None,
-           oracle=True):
+           oracle=True, workspace=True):
+    """One product through mx_launch_batched_matmul_ws with the workspace its query asks for
+    (workspace=False: the reference-signature entry point, which never splits K)."""
     a_shape = list(a_shape or a.shape)
     bt_shape = list(bt_shape or bt.shape)
     a_strides = a_strides or contiguous_strides(a_shape)
@@ -38,7 +40,9 @@ def run_mm(mx, orc, code, a, bt, a_shape=None, a_strides=None, bt_shape=None, bt
     A = mx.DeviceBuffer.from_numpy(a.reshape(-1))
     B = mx.DeviceBuffer.from_numpy(bt.reshape(-1))
     C = mx.DeviceBuffer(total * a.dtype.itemsize)
-    mx.launch_batched_matmul(code, desc, K, C.ptr, A.ptr, B.ptr)
+    wsb = mx.matmul_workspace_bytes(code, desc, K) if workspace else 0
+    W = mx.DeviceBuffer(wsb) if wsb else None
+    mx.launch_batched_matmul(code, desc, K, C.ptr, A.ptr, B.ptr, workspace=W.ptr if W else 0, workspace_bytes=wsb)
     mx.sync()
     got = C.download(a.dtype, total)
     if not oracle:          # the oracle reads K unit-stride (packed operands)
@@ -129,6 +133,48 @@ def test_split_k(mx, orc, dt, case):
     assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
     got2, _, _ = run_mm(mx, orc, code, a, bt)          # deterministic: the same bits again
     assert np.array_equal(got, got2)
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16"])
+def test_split_k_workspace_rules(mx, orc, dt):
+    """A product that splits K asks for a workspace; without one (the reference-signature entry
+    point, or a workspace one byte short) it runs unsplit, within the same tolerance, and no
+    call allocates device memory."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(14)
+    a_shape, bt_shape = [512, 4096], [10, 4096]
+    a = gen(rng, code, a_shape, 1.0 / 64, mx)
+    bt = gen(rng, code, bt_shape, 1.0, mx)
+    out, desc = matmul_desc(mx, a_shape, contiguous_strides(a_shape), bt_shape, contiguous_strides(bt_shape))
+    wsb = mx.matmul_workspace_bytes(code, desc, 4096)
+    assert wsb > 0 and wsb % (512 * 10 * 4) == 0
+    before = mx.alloc_stats()
+    split, ref, _ = run_mm(mx, orc, code, a, bt)
+    plain, _, _ = run_mm(mx, orc, code, a, bt, workspace=False)
+    A = mx.DeviceBuffer.from_numpy(a.reshape(-1))
+    B = mx.DeviceBuffer.from_numpy(bt.reshape(-1))
+    C = mx.DeviceBuffer(512 * 10 * a.dtype.itemsize)
+    W = mx.DeviceBuffer(wsb)
+    mx.launch_batched_matmul(code, desc, 4096, C.ptr, A.ptr, B.ptr, workspace=W.ptr, workspace_bytes=wsb - 1)
+    mx.sync()
+    short = C.download(a.dtype, 512 * 10)
+    assert np.array_equal(short, plain)                  # one byte short: the unsplit product
+    for got in (split, plain):
+        assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
+    # the only allocations were this test's own buffers: A, B, C and the workspace in the first
+    # run_mm, A, B and C in the second, four here
+    after = mx.alloc_stats()
+    assert after[0] - before[0] == 4 + 3 + 4
+
+
+@pytest.mark.parametrize("case", [([2048, 2048], [2048, 2048]), ([16, 2048, 2048], [2048, 2048]),
+                                  ([8, 1, 4096], [4096, 4096])])
+def test_no_workspace_when_tiles_fill_the_chip(mx, case):
+    """Products with enough output tiles, and the skinny kernel's shapes, never split."""
+    a_shape, bt_shape = case
+    out, desc = matmul_desc(mx, a_shape, contiguous_strides(a_shape), bt_shape, contiguous_strides(bt_shape))
+    for code in (mx.FLOAT32, mx.FLOAT16, mx.BFLOAT16, mx.INT32):
+        assert mx.matmul_workspace_bytes(code, desc, a_shape[-1]) == 0
 
 
 def test_split_k_strided(mx, orc):

@@ -39,12 +39,13 @@ def scalar_bits(mx, code, v):
     return x
 
 
-def unfused(mx, code, desc, K, out, A, Bt, bias, s, act, total, esz):
-    """The three launches the fused call replaces."""
+def unfused(mx, code, desc, K, out, A, Bt, bias, s, act, total, esz, W, wsb):
+    """The three launches the fused call replaces (the product with the same workspace, so it
+    splits K exactly as the fused call does)."""
     C = mx.DeviceBuffer(total * esz)
     Z = mx.DeviceBuffer(total * esz)
     H = mx.DeviceBuffer(total * esz)
-    mx.launch_batched_matmul(code, desc, K, C.ptr, A.ptr, Bt.ptr)
+    mx.launch_batched_matmul(code, desc, K, C.ptr, A.ptr, Bt.ptr, workspace=W.ptr if W else 0, workspace_bytes=wsb)
     N = out[-1]
     bd = mx.broadcast_shapes(list(out), contiguous_strides(out), [N], [1])
     d3 = mx.collapse_dims3(bd[2], bd[3], bd[5], bd[1])
@@ -77,8 +78,11 @@ def test_bias_act_equals_three_launches(mx, orc, dt, case, act, sval):
     C, Z, H = (mx.DeviceBuffer(total * esz) for _ in range(3))
     for B in (C, Z, H):
         B.fill_bytes(0xA5)
-    mx.launch_batched_matmul_bias_act(code, desc, K, C.ptr, A.ptr, Bt.ptr, bias.ptr, Z.ptr, act_op, s.ptr, H.ptr)
-    C1, Z1, H1 = unfused(mx, code, desc, K, out, A, Bt, bias, s, act_op, total, esz)
+    wsb = mx.matmul_workspace_bytes(code, desc, K)
+    W = mx.DeviceBuffer(wsb) if wsb else None
+    mx.launch_batched_matmul_bias_act(code, desc, K, C.ptr, A.ptr, Bt.ptr, bias.ptr, Z.ptr, act_op, s.ptr, H.ptr,
+                                      workspace=W.ptr if W else 0, workspace_bytes=wsb)
+    C1, Z1, H1 = unfused(mx, code, desc, K, out, A, Bt, bias, s, act_op, total, esz, W, wsb)
     mx.sync()
     npt = np_dtype(mx, code)
     got = [X.download(npt, total) for X in (C, Z, H)]

@@ -116,6 +116,26 @@ def test_reshaped_chain_axes_3_then_1(mx, orc, opn):
         assert np.array_equal(bits(got1), bits(ref1))
 
 
+@pytest.mark.parametrize("opn", ["RED_ARGMAX", "RED_ARGMIN", "RED_MAX", "RED_MIN", "RED_SUM"])
+def test_reshaped_axis1_full(mx, orc, opn):
+    """Every reduction over axis 1 of the whole X.reshape(64,4,4096,16) (the arg-reductions' second
+    axis of the workload), with 30% of the axis-1 rows carrying duplicated extrema (first index
+    wins), against the oracle."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal([64, 4, 4096, 16]).astype(np.float32)
+    x = inject_ties(rng, x, 1, minimum=op in (mx.RED_MIN, mx.RED_ARGMIN))
+    got, ref, desc, *_ = run_reduce(mx, orc, op, mx.FLOAT32, x.ravel(), [64, 4, 4096, 16], 1)
+    assert desc == [[64, 65536], [65536, 1], [262144, 1]]
+    if op == mx.RED_SUM:
+        check_sum(got, ref, np.abs(x.astype(np.float64)).sum(1).ravel())
+    else:
+        assert np.array_equal(bits(got), bits(ref))
+        if op in (mx.RED_ARGMAX, mx.RED_ARGMIN):      # first index of the extremum, as numpy's
+            npf = np.argmax if op == mx.RED_ARGMAX else np.argmin
+            assert np.array_equal(got, npf(x, axis=1).ravel().astype(np.int32))
+
+
 def test_add_rowsum_sum(mx, orc):
     rng = np.random.default_rng(0)
     a = rng.standard_normal([4096, 1024]).astype(np.float32)
