@@ -124,6 +124,19 @@ int mx_launch_reduce(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduc
                      void* out, const void* in, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/* No counterpart in the reference: mx_launch_reduce for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * takes no workspace: a reduction whose axis is split over blocks keeps its partials in a fixed
+ * 4 MiB device array that the library holds on each GPU until the process ends (set up by
+ * mx_hip_init for its device).  Reductions needing more than that (mx_reduce_workspace_bytes
+ * above 4 MiB) fail with MX_ERR_WORKSPACE.  Outputs equal mx_launch_reduce's bit for bit.  The
+ * call allocates nothing.  Every call on one GPU shares that array: calls that overlap in time
+ * on one GPU (two streams, two threads) race, so issue them on one stream. */
+#define MX_REDUCE_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
+int mx_launch_reduce_noalloc(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduce,
+                             int cdims, const uint32_t* shape, const uint32_t* sOut, const uint32_t* sIn,
+                             void* out, const void* in, void* stream);
+
 /* n (<= MX_REDUCE_GROUP_MAX) reductions of one dtype over one descriptor (the arguments of
  * mx_launch_reduce), member k with its own op ops[k], input ins[k], output outs[k] and workspace
  * workspaces[k] of workspace_bytes[k] bytes (its mx_reduce_workspace_bytes; the two arrays may be

@@ -83,6 +83,7 @@ _SIGS = {
     "mx_launch_bcast_binary": ([_i, _i, _i, _u32p, _u32p, _u32p, _u32p, _vp, _vp, _vp, _vp], _i),
     "mx_reduce_workspace_bytes": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, ctypes.POINTER(_sz)], _i),
     "mx_launch_reduce": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp, _sz, _vp], _i),
+    "mx_launch_reduce_noalloc": ([_i, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, _vp, _vp, _vp], _i),
     "mx_launch_reduce_group": ([_i, _ip, _i, _u32, _u32, _i, _u32p, _u32p, _u32p, ctypes.POINTER(_vp),
                                 ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_sz), _vp], _i),
     "mx_collapse_dims3": ([_u32p, _u32p, _u32p, _u32p, _u32, _u64, _u32p, _u32p, _u32p, _u32p, _u32p], _i),
@@ -373,6 +374,17 @@ def launch_reduce(op, dtype, reduce_stride, n_reduce, desc, out, inp, workspace=
     shape, sOut, sIn = desc
     check(lib.mx_launch_reduce(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut), u32(sIn),
                                int(out), int(inp), int(workspace), workspace_bytes, stream))
+
+
+REDUCE_NOALLOC_SCRATCH_BYTES = 4 << 20
+
+
+def launch_reduce_noalloc(op, dtype, reduce_stride, n_reduce, desc, out, inp, stream=None):
+    """mx_launch_reduce_noalloc: launch_reduce without a workspace (split partials in the
+    library's fixed per-GPU scratch; calls on one GPU must not overlap in time)."""
+    shape, sOut, sIn = desc
+    check(lib.mx_launch_reduce_noalloc(op, dtype, reduce_stride, n_reduce, len(shape), u32(shape), u32(sOut),
+                                       u32(sIn), int(out), int(inp), stream))
 
 
 def _group_arrays(ops, outs, ins, workspaces, workspace_bytes):

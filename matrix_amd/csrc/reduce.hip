@@ -3,6 +3,8 @@
 // reduce_plans.hpp.
 #include "reduce_plans.hpp"
 
+#include <mutex>
+
 namespace mx {
 namespace {
 
@@ -164,6 +166,72 @@ int run(const Desc& d, void* outp, const void* inp, void* ws, size_t ws_bytes, h
 
 
 using namespace mx;
+
+// ------------------------------------------------------------------ the allocation-free form
+// mx_launch_reduce_noalloc takes its split partials from `scratch`, a fixed device array instead
+// of a caller workspace.  Host code never passes `scratch` itself (in host code the name is a
+// host-side stand-in, not a device address): mx_hip_init looks up each device's own address of
+// the array once, with that device current, and the entry point passes that address.  The
+// partials are written by the first launch before the combine launch reads them, so nothing in
+// the array has to start at zero.
+namespace mx {
+constexpr size_t kNoallocScratchBytes = (size_t)4 << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace mx
+
+static __device__ __align__(256) unsigned char scratch[mx::kNoallocScratchBytes];
+
+namespace mx {
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// Called by mx_hip_init with `device` current.
+int reduce_noalloc_setup(int device) {
+    if (device < 0 || device >= kMaxDevices)
+        return fail(MX_ERR_UNSUPPORTED, "mx_hip_init: device " + std::to_string(device) + " beyond the " +
+                                            std::to_string(kMaxDevices) + " this library tracks");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return MX_OK;
+    void* ptr = nullptr;
+    MX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail(MX_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[device] = ptr;
+    return MX_OK;
+}
+
+}  // namespace mx
+
+extern "C" int mx_launch_reduce_noalloc(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduce, int cdims,
+                                        const uint32_t* shape, const uint32_t* sOut, const uint32_t* sIn, void* out,
+                                        const void* in, void* stream) {
+    size_t need = 0;
+    int rc = mx_reduce_workspace_bytes(op, dtype, reduce_stride, n_reduce, cdims, shape, sOut, sIn, &need);
+    if (rc != MX_OK) return rc;
+    if (need > kNoallocScratchBytes)
+        return fail(MX_ERR_WORKSPACE, "mx_launch_reduce_noalloc: this reduction needs " + std::to_string(need) +
+                                          " bytes of split partials, above the fixed " +
+                                          std::to_string(kNoallocScratchBytes) +
+                                          " (use mx_launch_reduce with a workspace)");
+    void* ws = nullptr;
+    if (need > 0) {
+        // the array of the GPU the launch runs on: the stream's device
+        hipStream_t st;
+        if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+        hipDevice_t dev = -1;
+        MX_HIP(hipStreamGetDevice(st, &dev));
+        {
+            std::lock_guard<std::mutex> lk(g_scratch_mu);
+            if (dev >= 0 && dev < kMaxDevices) ws = g_scratch_ptr[dev];
+        }
+        if (!ws)
+            return fail(MX_ERR_NOT_INITIALIZED, "mx_launch_reduce_noalloc: device " + std::to_string(dev) +
+                                                    " was not set up by mx_hip_init");
+    }
+    return mx_launch_reduce(op, dtype, reduce_stride, n_reduce, cdims, shape, sOut, sIn, out, in, ws,
+                            ws ? kNoallocScratchBytes : 0, stream);
+}
 
 extern "C" int mx_reduce_workspace_bytes(int op, int dtype, uint32_t reduce_stride, uint32_t n_reduce,
                                          int cdims, const uint32_t* shape, const uint32_t* sOut,

@@ -60,6 +60,10 @@ namespace {
 std::atomic<uint64_t> g_allocs{0}, g_frees{0};
 }  // namespace
 
+// Looks up this device's address of the fixed scratch of mx_launch_reduce_noalloc (reduce.hip),
+// once per device, with the device current.
+int reduce_noalloc_setup(int device);
+
 }  // namespace mx
 
 using namespace mx;
@@ -88,6 +92,8 @@ int mx_hip_init(int device) {
     std::string arch = prop.gcnArchName;
     if (arch.rfind("gfx950", 0) != 0)
         return fail(MX_ERR_UNSUPPORTED, "mx_hip_init: kernels are built for gfx950, device is " + arch);
+    const int rc = reduce_noalloc_setup(device);
+    if (rc != MX_OK) return rc;
     g_device.store(device);
     return MX_OK;
 }
