@@ -223,7 +223,8 @@ def _normal(rng, shape, scale, dt):
 
 def config_add_rowsum(mx):
     """Config 1: C = A[4096,1024] + B[1,1024] (broadcast), s = C.sum(1); 20 rotated copies of A
-    (320 MiB, more than the Infinity Cache)."""
+    (320 MiB, more than the Infinity Cache).  The graph executor fuses the two nodes into one launch
+    (C still written); GB/s and frac_hbm count the bytes that launch moves (33,574,912)."""
     rng = np.random.default_rng(0)
     a = rng.standard_normal([4096, 1024], dtype=np.float32)
     b = rng.uniform(-1, 1, [1, 1024]).astype(np.float32)
@@ -247,15 +248,46 @@ def config_add_rowsum(mx):
     def graph_fused(i=0):
         fused(C[i % 2].ptr, A[i % 20].ptr, B.ptr, S.ptr)
 
-    nbytes = 50_352_128
+    graph_bytes, moved = 50_352_128, 33_574_912
     ms2 = _timed(mx, graph, 40)
     ms = _timed(mx, graph_fused, 40)
-    gbs = nbytes / (ms * 1e-3) / 1e9
+    gbs = moved / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-            "bytes": nbytes, "hbm_bytes": 33_574_912, "hbm_GB/s": round(33_574_912 / (ms * 1e-3) / 1e9, 1),
-            "unfused_ms": round(ms2, 5), "unfused_GB/s": round(nbytes / (ms2 * 1e-3) / 1e9, 1),
-            "note": "the graph's add and row sum fused into one launch (C written, read back from registers); "
-                    "GB/s counts the unfused graph's 50,352,128 algorithmic bytes, hbm_GB/s the 33,574,912 moved"}
+            "hbm_bytes": moved, "graph_bytes": graph_bytes,
+            "graph_GB/s": round(graph_bytes / (ms * 1e-3) / 1e9, 1),
+            "unfused_ms": round(ms2, 5), "unfused_GB/s": round(graph_bytes / (ms2 * 1e-3) / 1e9, 1),
+            "note": "the graph's add and row sum fused into one launch (C written, its rows reduced from "
+                    "registers); GB/s / frac_hbm over the 33,574,912 bytes that launch moves, graph_GB/s over "
+                    "the unfused graph's 50,352,128 algorithmic bytes, unfused_* the two launches",
+            "_cpu_inputs": (a, b, desc, rdesc)}
+
+
+def matmul_case(mx, dt, kind, rng):
+    """(launch(i), flop or bytes, host operands, descriptor, K) of config 3's main product
+    A[16,2048,2048] x B[2048,2048] (kind "main") or the skinny A[8,1,4096] x B[4096,4096]."""
+    code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
+    if kind == "main":
+        a = _normal(rng, [16, 2048, 2048], 1 / np.sqrt(2048), dt)
+        bt = _normal(rng, [2048, 2048], 1 / np.sqrt(2048), dt)
+        desc = ([16, 2048, 2048], [2048 * 2048, 2048, 1], [0, 2048, 1], [2048 * 2048, 2048, 1])
+        K, copies = 2048, 1
+    else:
+        a = _normal(rng, [8, 1, 4096], 1 / 64, dt)
+        bt = _normal(rng, [4096, 4096], 1 / 64, dt)
+        desc = ([8, 1, 4096], [4096, 4096, 1], [0, 4096, 1], [4096, 4096, 1])
+        K, copies = 4096, (8 if dt == "f32" else 12)     # rotated copies of B: 256 MiB and more
+    A = mx.DeviceBuffer.from_numpy(a)
+    Bs = [mx.DeviceBuffer.from_numpy(bt) for _ in range(copies)]
+    C = mx.DeviceBuffer(int(np.prod(desc[0])) * a.itemsize)
+    wsb = mx.matmul_workspace_bytes(code, desc, K)
+    W = mx.DeviceBuffer(wsb) if wsb else None
+    mm = mx.prepare_batched_matmul(code, desc, K, workspace=W.ptr if W else 0, workspace_bytes=wsb)
+    keep = (A, Bs, C, W)
+
+    def launch(i=0):
+        mm(C.ptr, A.ptr, Bs[i % copies].ptr)
+    launch.keep = keep
+    return launch, (a, bt, desc, K, code)
 
 
 def config_matmul(mx):
@@ -263,34 +295,73 @@ def config_matmul(mx):
     fp32 accumulation; skinny A[8,1,4096] x B[4096,4096].  B^T is packed once (dot's copy) and
     the timed launches are the batched-matmul kernel alone."""
     rng = np.random.default_rng(1)
-    res = {}
+    res, cpu_in = {}, {}
     for dt in ("f32", "f16"):
-        code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
-        a = _normal(rng, [16, 2048, 2048], 1 / np.sqrt(2048), dt)
-        bt = _normal(rng, [2048, 2048], 1 / np.sqrt(2048), dt)
-        A, Bt = mx.DeviceBuffer.from_numpy(a), mx.DeviceBuffer.from_numpy(bt)
-        C = mx.DeviceBuffer(16 * 2048 * 2048 * a.itemsize)
-        desc = ([16, 2048, 2048], [2048 * 2048, 2048, 1], [0, 2048, 1], [2048 * 2048, 2048, 1])
-        mm = mx.prepare_batched_matmul(code, desc, 2048)
-        ms = _timed(mx, lambda i=0: mm(C.ptr, A.ptr, Bt.ptr), 5 if dt == "f32" else 20)
+        launch, host = matmul_case(mx, dt, "main", rng)
+        ms = _timed(mx, launch, 5 if dt == "f32" else 20)
         tf = 274_877_906_944 / (ms * 1e-3) / 1e12
         res[f"main_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
                              "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)}
-        del A, Bt, C
-        # skinny: 8 copies of B rotated (256 MiB and more), bytes = A + B + C
-        a = _normal(rng, [8, 1, 4096], 1 / 64, dt)
-        bt = _normal(rng, [4096, 4096], 1 / 64, dt)
-        A = mx.DeviceBuffer.from_numpy(a)
-        Bs = [mx.DeviceBuffer.from_numpy(bt) for _ in range(8 if dt == "f32" else 12)]
-        C = mx.DeviceBuffer(8 * 4096 * a.itemsize)
-        desc = ([8, 1, 4096], [4096, 4096, 1], [0, 4096, 1], [4096, 4096, 1])
-        mm = mx.prepare_batched_matmul(code, desc, 4096)
-        ms = _timed(mx, lambda i=0: mm(C.ptr, A.ptr, Bs[i % len(Bs)].ptr), 40)
+        cpu_in[f"main_{dt}"] = host
+        del launch
+        launch, host = matmul_case(mx, dt, "skinny", rng)
+        a, bt = host[0], host[1]
+        ms = _timed(mx, launch, 40)
         nbytes = (a.size + bt.size + 8 * 4096) * a.itemsize
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[f"skinny_{dt}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-        del A, Bs, C
+        cpu_in[f"skinny_{dt}"] = host
+        del launch
+    res["_cpu_inputs"] = cpu_in
     return res
+
+
+def _cs(shape):
+    st, acc = [0] * len(shape), 1
+    for i in range(len(shape) - 1, -1, -1):
+        st[i] = acc
+        acc *= shape[i]
+    return st
+
+
+CONV_CASES = {"3x3": (32, 64, 56, 56, 128, 3, 1, 1), "1x1s2": (32, 256, 28, 28, 512, 1, 0, 2)}
+
+
+def conv_geom(name, layout):
+    """Channels-last geometry of config 4's case `name`: NCHW-stored tensors seen through the
+    reference conv2d's transpose(0,2,3,1) views ("nchw"), or stored NHWC / OHWI ("nhwc")."""
+    n, c, h, w, o, k, pad, stride = CONV_CASES[name]
+    oh = (h + 2 * pad - k) // stride + 1
+    ow = (w + 2 * pad - k) // stride + 1
+    if layout == "nchw":
+        st = _cs([n, c, h, w])
+        in_st = [st[0], st[2], st[3], st[1]]
+        kst = _cs([o, c, k, k])
+        k_st = [kst[0], kst[2], kst[3], kst[1]]
+    else:
+        in_st, k_st = _cs([n, h, w, c]), _cs([o, k, k, c])
+    return dict(in_shape=[n, h, w, c], k_shape=[o, k, k, c], out_shape=[n, oh, ow, o], in_strides=in_st,
+                k_strides=k_st, out_strides=_cs([n, oh, ow, o]), pad=[pad, pad], stride=[stride, stride])
+
+
+def conv_case(mx, dt, name, layout, rng):
+    """(launch(i), flop, host operands) of one config-4 convolution (packing inside the call)."""
+    code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
+    n, c, h, w, o, k, pad, stride = CONV_CASES[name]
+    geom = conv_geom(name, layout)
+    x = _normal(rng, [n, c, h, w] if layout == "nchw" else [n, h, w, c], 1.0, dt)
+    wt = _normal(rng, [o, c, k, k] if layout == "nchw" else [o, k, k, c], np.sqrt(2.0 / (c * k * k)), dt)
+    X, W = mx.DeviceBuffer.from_numpy(x), mx.DeviceBuffer.from_numpy(wt)
+    Y = mx.DeviceBuffer(int(np.prod(geom["out_shape"])) * x.itemsize)
+    wsb = mx.conv_workspace_bytes(code, geom)
+    WS = mx.DeviceBuffer(max(wsb, 256))
+    conv = mx.prepare_conv_nd(code, geom, WS.ptr, wsb)
+
+    def launch(i=0):
+        conv(Y.ptr, X.ptr, W.ptr)
+    launch.keep = (X, W, Y, WS)
+    flop = 2.0 * np.prod(geom["out_shape"]) * c * k * k
+    return launch, flop, (x, wt, geom, code)
 
 
 def config_conv(mx):
@@ -298,46 +369,19 @@ def config_conv(mx):
     conv2d sees them (NHWC / OHWI transposed views: packing is part of the timed call) and
     natively channels-last; 1x1 stride 2: x [32,256,28,28] * w [512,256,1,1]."""
     rng = np.random.default_rng(2)
-
-    def cs(shape):
-        st, acc = [0] * len(shape), 1
-        for i in range(len(shape) - 1, -1, -1):
-            st[i] = acc
-            acc *= shape[i]
-        return st
-
-    res = {}
+    res, cpu_in = {}, {}
     for dt in ("f32", "f16"):
-        code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
-        for name, (n, c, h, w, o, k, pad, stride), layouts in (
-                ("3x3", (32, 64, 56, 56, 128, 3, 1, 1), ("nchw", "nhwc")),
-                ("1x1s2", (32, 256, 28, 28, 512, 1, 0, 2), ("nchw",))):
-            oh = (h + 2 * pad - k) // stride + 1
-            ow = (w + 2 * pad - k) // stride + 1
-            x = _normal(rng, [n, c, h, w], 1.0, dt)
-            wt = _normal(rng, [o, c, k, k], np.sqrt(2.0 / (c * k * k)), dt)
-            X, W = mx.DeviceBuffer.from_numpy(x), mx.DeviceBuffer.from_numpy(wt)
-            Y = mx.DeviceBuffer(n * oh * ow * o * x.itemsize)
+        for name, layouts in (("3x3", ("nchw", "nhwc")), ("1x1s2", ("nchw", "nhwc"))):
             for layout in layouts:
-                if layout == "nchw":
-                    st = cs([n, c, h, w])
-                    in_st = [st[0], st[2], st[3], st[1]]
-                    kst = cs([o, c, k, k])
-                    k_st = [kst[0], kst[2], kst[3], kst[1]]
-                else:
-                    in_st, k_st = cs([n, h, w, c]), cs([o, k, k, c])
-                geom = dict(in_shape=[n, h, w, c], k_shape=[o, k, k, c], out_shape=[n, oh, ow, o], in_strides=in_st,
-                            k_strides=k_st, out_strides=cs([n, oh, ow, o]), pad=[pad, pad], stride=[stride, stride])
-                wsb = mx.conv_workspace_bytes(code, geom)
-                WS = mx.DeviceBuffer(max(wsb, 256))
-                conv = mx.prepare_conv_nd(code, geom, WS.ptr, wsb)
-                ms = _timed(mx, lambda i=0: conv(Y.ptr, X.ptr, W.ptr), 20)
-                flop = 2.0 * n * oh * ow * o * c * k * k
+                launch, flop, host = conv_case(mx, dt, name, layout, rng)
+                ms = _timed(mx, launch, 20)
                 tf = flop / (ms * 1e-3) / 1e12
                 res[f"{name}_{layout}_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
                                                 "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)}
-                del WS
-            del X, W, Y
+                if layout == "nchw":
+                    cpu_in[f"{name}_{dt}"] = host
+                del launch
+    res["_cpu_inputs"] = cpu_in
     return res
 
 
@@ -368,6 +412,32 @@ def config_mlp():
     return r
 
 
+def cpu_info():
+    """The host CPU model and its core counts, stated with every CPU baseline."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+
+
+def _cpu_median(fn, reps, budget_s):
+    """Median wall time of fn() over reps runs (fewer when the budget runs out, at least one)."""
+    times, t_all = [], time.perf_counter()
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > budget_s:
+            break
+    return float(np.median(times)), len(times)
+
+
 def run_cpu_baseline(mx_collapse):
     """The oracle (the reference's CPU loops restated) single-threaded on the host: the whole
     step's ops on the same X, repeated until about 10 s of CPU time; GB/s of algorithmic bytes."""
@@ -387,7 +457,143 @@ def run_cpu_baseline(mx_collapse):
         if dt > 10.0 or reps >= 40:
             break
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"the full step (all ops on X[256,65536] f32) x{reps}, {dt:.2f} s single-threaded"}
+            "sample": f"the full step (all ops on X[256,65536] f32) x{reps}, {dt:.2f} s single-threaded",
+            **cpu_info()}
+
+
+def cpu_add_rowsum(orc, inputs):
+    """Config 1 on the oracle, single-threaded: the add then the row sum (the reference's two
+    CPU loops), median of 5; GB/s over the graph's 50,352,128 algorithmic bytes."""
+    a, b, desc, rdesc = inputs
+
+    def run():
+        c = orc.bcast_binary(orc.ADD, orc.F32, desc, a.size, a.ravel(), b.ravel())
+        orc.reduce(orc.RSUM, orc.F32, 1, 1024, rdesc, 4096, c, nthreads=1)
+    sec, n = _cpu_median(run, 5, 20.0)
+    return {"value": round(50_352_128 / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"the whole graph (add + row sum of A[4096,1024]), median of {n}", **cpu_info()}
+
+
+def cpu_matmul(orc, name, host):
+    """Config 3 on the oracle, single-threaded, on a bounded sample: the main product's first 128
+    (f32) or 32 (f16) rows of batch 0 (of 32768 rows), the skinny product whole.  f16 runs the reference's literal
+    loop (half accumulator)."""
+    a, bt, desc, K, code = host
+    oc = orc.F32 if code == 0 else orc.F16
+    if name.startswith("main"):
+        rows = 128 if code == 0 else 32        # the literal half-accumulator loop is ~15x slower
+        av = np.ascontiguousarray(a.reshape(-1, K)[:rows])
+        d = ([rows, 2048], [K, 1], [K, 1], [2048, 1])
+        flop = 2.0 * rows * 2048 * K
+        sample = f"rows 0-{rows - 1} of batch 0 ({rows} x 2048 x {K}, {flop / 1e9:.2f} GFLOP)"
+        total = rows * 2048
+    else:
+        av, d = a.reshape(-1), desc
+        flop = 2.0 * 8 * 4096 * K
+        sample = f"the whole product ({flop / 1e9:.2f} GFLOP)"
+        total = 8 * 4096
+    fn = (lambda: orc.batched_matmul(oc, d, K, av.reshape(-1), bt.reshape(-1), total, acc=orc.ACC_LITERAL,
+                                     nthreads=1))
+    sec, n = _cpu_median(fn, 3, 6.0)
+    out = {"value": round(flop / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+           "sample": f"{sample}, median of {n}", **cpu_info()}
+    if not name.startswith("main"):
+        nbytes = (a.size + bt.size + 8 * 4096) * a.itemsize
+        out["GB/s"] = round(nbytes / sec / 1e9, 3)
+    return out
+
+
+def cpu_conv(orc, name, host):
+    """Config 4 on the oracle, single-threaded, on a bounded sample: the first image(s) of the
+    batch of 32, on the same NHWC / OHWI views of the NCHW tensors."""
+    x, wt, geom, code = host
+    oc = orc.F32 if code == 0 else orc.F16
+    n_img = 1 if name.startswith("3x3") else (4 if code == 0 else 2)
+    g = dict(geom)
+    g["in_shape"] = [n_img] + geom["in_shape"][1:]
+    g["out_shape"] = [n_img] + geom["out_shape"][1:]
+    c = geom["in_shape"][-1]
+    per_img = int(np.prod(geom["in_shape"][1:]))
+    xs = np.ascontiguousarray(x.reshape(-1)[:n_img * per_img])       # NCHW: images are contiguous
+    kk = geom["k_shape"][1] * geom["k_shape"][2]
+    flop = 2.0 * np.prod(g["out_shape"]) * c * kk
+    total = int(np.prod(g["out_shape"]))
+    fn = (lambda: orc.conv(oc, g["in_shape"], g["k_shape"], g["out_shape"], g["in_strides"], g["k_strides"],
+                           _cs(g["out_shape"]), g["pad"], g["stride"], [1, 1], [1, 1], 1, 0, xs, wt.reshape(-1),
+                           total, acc=orc.ACC_LITERAL, nthreads=1))
+    sec, n = _cpu_median(fn, 3, 6.0)
+    return {"value": round(float(flop / sec / 1e12), 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{n_img} of 32 images ({flop / 1e9:.2f} GFLOP), median of {n}", **cpu_info()}
+
+
+def cpu_mlp(orc, batch=32):
+    """Config 5 on the oracle, single-threaded: one training step of the same MLP at a batch of
+    `batch` rows instead of 512 (the step's every op in the reference's CPU loops: the B^T copy
+    dot makes before each product, the products, bias adds, the ReLU's Max and its four-node
+    gradient, the loss and the bias gradients' column sums); steps/s at that batch and its
+    TFLOP/s."""
+    rng = np.random.default_rng(0)
+    D = [1024, 4096, 4096, 10]
+    B = batch
+    F = orc.F32
+    x = rng.standard_normal([B, D[0]], dtype=np.float32)
+    t = rng.uniform(0, 1, [B, D[3]]).astype(np.float32)
+    W = [(rng.standard_normal([D[l], D[l + 1]], dtype=np.float32) / np.sqrt(D[l])).astype(np.float32)
+         for l in range(3)]
+    bias = [np.zeros(D[l + 1], np.float32) for l in range(3)]
+    zero = np.zeros(1, np.float32)
+    one = np.ones(1, np.float32)
+
+    def tr(m, r, c):          # contiguous copy of the transpose of m [r, c] (dot's B^T pack)
+        return orc.copy_strided(F, F, [c, r], [r, 1], [1, c], np.empty(r * c, np.float32), m.reshape(-1))
+
+    def mm(a, bt, M, N, K):   # a [M, K] . bt [N, K]^T
+        return orc.batched_matmul(F, ([M, N], [K, 1], [K, 1], [N, 1]), K, a.reshape(-1), bt.reshape(-1), M * N,
+                                  nthreads=1)
+
+    def ew(op, a, b, n, b_scalar=False):
+        return orc.bcast_binary(op, F, ([n], [1], [0 if b_scalar else 1], [1]), n, a.reshape(-1), b.reshape(-1))
+
+    def add_rows(z, b, M, N):
+        return orc.bcast_binary(orc.ADD, F, ([M, N], [N, 1], [0, 1], [N, 1]), M * N, z.reshape(-1), b)
+
+    def col_sum(g, M, N):
+        return orc.reduce(orc.RSUM, F, N, M, ([N], [1], [1]), N, g.reshape(-1), nthreads=1)
+
+    def step():
+        hs, zs, wts = [x], [], []
+        for l in range(3):
+            wt = tr(W[l], D[l], D[l + 1])
+            wts.append(wt)
+            z = add_rows(mm(hs[-1], wt, B, D[l + 1], D[l]), bias[l], B, D[l + 1])
+            zs.append(z)
+            hs.append(ew(orc.MAX, z, zero, B * D[l + 1], True) if l < 2 else z)
+        n3 = B * D[3]
+        d = ew(orc.SUB, hs[-1], t, n3)
+        sq = ew(orc.MUL, d, d, n3)
+        orc.reduce(orc.RSUM, F, 1, n3, ([1], [1], [n3]), 1, sq, nthreads=1)
+        g = ew(orc.MUL, np.ones(n3, np.float32), d, n3)
+        g = ew(orc.ADD, g, g, n3)                          # d(d*d) = g*d + g*d
+        for l in (2, 1, 0):
+            N, K = D[l + 1], D[l]
+            col_sum(g, B, N)                               # bias gradient
+            gt = tr(g, B, N)                               # g^T [N, B]
+            ht = tr(hs[l], B, K)                           # h^T [K, B]
+            mm(gt, ht, N, K, B)                            # (dW)^T = g^T . h
+            if l > 0:
+                ga = mm(g, tr(wts[l], N, K), B, K, N)      # g . W^T (dot packs W again)
+                # the ReLU's vjp: mask = equal(0, max(z, 0)), g * (1 - mask) (primitives.cpp:2604-2608)
+                m = ew(orc.MAX, zs[l - 1], zero, B * K, True)
+                mask = orc.bcast_binary(orc.EQ, F, ([B * K], [0], [1], [1]), B * K, zero, m)
+                keep = orc.bcast_binary(orc.SUB, F, ([B * K], [0], [1], [1]), B * K, one, mask)
+                g = ew(orc.MUL, ga, keep, B * K)
+
+    sec, n = _cpu_median(step, 3, 8.0)
+    fwd = 2.0 * B * (D[0] * D[1] + D[1] * D[2] + D[2] * D[3])
+    flop = fwd + 2.0 * fwd - 2.0 * B * D[0] * D[1]
+    return {"value": round(1.0 / sec, 3), "unit": f"steps/s at batch {B}", "TFLOP/s": round(flop / sec / 1e12, 6),
+            "cores": 1, "kind": "port",
+            "sample": f"one training step at batch {B} of 512 ({flop / 1e9:.2f} GFLOP), median of {n}", **cpu_info()}
 
 
 def measured_traffic(op_name):
@@ -402,12 +608,33 @@ def measured_traffic(op_name):
     return rec["traffic_bytes"] if rec else None
 
 
+MFMA_PROBES = {
+    "matmul_main_f32": ("matmul", "f32", "main"), "matmul_main_f16": ("matmul", "f16", "main"),
+    "conv_3x3_nhwc_f16": ("conv", "f16", "3x3", "nhwc"), "conv_3x3_nchw_f16": ("conv", "f16", "3x3", "nchw"),
+    "conv_3x3_nhwc_f32": ("conv", "f32", "3x3", "nhwc"), "conv_1x1s2_nchw_f16": ("conv", "f16", "1x1s2", "nchw"),
+}
+
+
 def kernel_probe(op_name, reps=10):
-    """For hardware-counter runs: only `op_name` of the reductions workload -- one op, or a group
-    launch (group_axis1, group_r4_axis3, ...) -- reps launches on rotated copies, then a 256 MiB
-    device copy (the calibration kernel of known bytes)."""
+    """For hardware-counter runs: only `op_name` -- an op or a group launch of the reductions
+    workload (group_axis1, group_r4_axis3, ...) followed by a 256 MiB device copy (the calibration
+    kernel of known bytes), or one of the matmul / convolution launches of MFMA_PROBES -- reps
+    launches."""
     import matrix_amd as mx
     mx.init(0)
+    if op_name in MFMA_PROBES:
+        spec = MFMA_PROBES[op_name]
+        rng = np.random.default_rng(1)
+        if spec[0] == "matmul":
+            launch, _ = matmul_case(mx, spec[1], spec[2], rng)
+            flop = 274_877_906_944
+        else:
+            launch, flop, _ = conv_case(mx, spec[1], spec[2], spec[3], rng)
+        for i in range(reps):
+            launch(i)
+        mx.sync()
+        print(json.dumps({"probe": op_name, "launches": reps, "flop_per_launch": float(flop)}), flush=True)
+        return
     x = make_input(0)
     copies = [mx.DeviceBuffer.from_numpy(x) for _ in range(N_COPIES)]
     prepared = [Prepared(mx, *o) for o in build_ops(mx)]
@@ -442,8 +669,8 @@ def kernel_probe(op_name, reps=10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--kernel-probe", default=None, metavar="OP",
-                    help="run only OP (an op or a group launch) of the reductions workload and a calibration "
-                         "copy (for counter runs)")
+                    help="run only OP (an op or a group launch of the reductions workload, then a calibration "
+                         "copy; or a matmul / convolution launch: " + ", ".join(MFMA_PROBES) + ") for counter runs")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
@@ -466,6 +693,18 @@ def main():
         configs["matmul"] = config_matmul(mx)
         configs["conv2d"] = config_conv(mx)
         configs["mlp_step_f32"] = config_mlp()
+        cpu_in = {"add": configs["add_rowsum_f32"].pop("_cpu_inputs"), "matmul": configs["matmul"].pop("_cpu_inputs"),
+                  "conv": configs["conv2d"].pop("_cpu_inputs")}
+        if not args.no_cpu_baseline:
+            # every config's CPU baseline: the oracle single-threaded on a bounded sample of that workload
+            from oracle import oracle as orc
+            orc.load()
+            configs["add_rowsum_f32"]["cpu_baseline"] = cpu_add_rowsum(orc, cpu_in["add"])
+            for k, host in cpu_in["matmul"].items():
+                configs["matmul"][k]["cpu_baseline"] = cpu_matmul(orc, k, host)
+            for k, host in cpu_in["conv"].items():
+                configs["conv2d"][k.replace("_", "_nchw_")]["cpu_baseline"] = cpu_conv(orc, k, host)
+            configs["mlp_step_f32"]["cpu_baseline"] = cpu_mlp(orc)
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(r["cpu_ops"])
     if int(g["step_bytes"]) != r["step_bytes"]:
         raise SystemExit(f"bench.py: step bytes differ ({g['step_bytes']} vs {r['step_bytes']})")
