@@ -154,7 +154,7 @@ void init(int device) {
 }
 
 Storage::~Storage() {
-    if (dev) mx_hip_free(dev);
+    if (dev && !borrowed) mx_hip_free(dev);
 }
 
 void Storage::allocate() {
@@ -208,14 +208,86 @@ matrix matrix::full(const std::vector<size_m>& shape, double value, dtype type) 
 }
 
 
+namespace {
+uint64_t g_epoch = 1;     // versions of leaves changed on the host (mark_changed)
+
+// A leaf whose values live on the device only (make_leaf / releaseTape of an evaluated node)
+// gets them on the host, which becomes their source.
+void take_to_host(Storage& st) {
+    if (st.host_is_source) return;
+    st.host.assign(st.bytes, 0);
+    if (st.bytes && st.dev) check(mx_hip_d2h(st.host.data(), st.dev, st.bytes, nullptr), "device-to-host copy");
+    st.host_is_source = true;
+    st.dev_stale = false;
+}
+}  // namespace
+
 void* matrix::host_data() {
-    if (tape || !storage || !storage->host_is_source) throw std::logic_error("matrix::host_data: not a leaf");
+    if (tape || !storage) throw std::logic_error("matrix::host_data: not a leaf");
+    if (storage->borrowed) throw std::logic_error("matrix::host_data: a compiled graph's input placeholder");
+    take_to_host(*storage);
     return storage->host.data();
 }
 
 void matrix::mark_changed() {
     if (tape || !storage) throw std::logic_error("matrix::mark_changed: not a leaf");
+    take_to_host(*storage);
     storage->dev_stale = true;
+    storage->leaf_version = ++g_epoch;
+}
+
+matrix matrix::leaf_scalar(float value, dtype type) { return scalar(value, type); }
+
+void matrix::releaseTape() {
+    if (!tape) return;
+    if (!tape->evaluated) throw std::logic_error("matrix::releaseTape: the node is not evaluated");
+    tape.reset();
+    storage->host_is_source = false;    // the device holds the values
+    storage->dev_stale = false;
+}
+
+void matrix::make_leaf() {
+    if (tape && !tape->evaluated) eval();
+    releaseTape();
+}
+
+void* matrix::host_view() {
+    if (!storage) throw std::logic_error("matrix::at: empty matrix");
+    if (storage->host_is_source) return storage->host.data();     // a leaf, or a view of one
+    if (!tape) {
+        take_to_host(*storage);
+        return storage->host.data();
+    }
+    if (!tape->evaluated) eval();
+    if (storage->host_version != storage->dev_version || storage->host.size() != storage->bytes) {
+        storage->host.resize(storage->bytes);
+        if (storage->bytes) check(mx_hip_d2h(storage->host.data(), storage->dev, storage->bytes, nullptr), "device-to-host copy");
+        storage->host_version = storage->dev_version;
+    }
+    return storage->host.data();
+}
+
+bool Primitive::invalidate_pass(uint64_t current_pass_id) {
+    if (last_visited_pass_id == current_pass_id) return !evaluated;
+    last_visited_pass_id = current_pass_id;
+    bool inv = false;
+    uint64_t nv = version;
+    for (uint32_t i = 0; i < num_inputs(); i++) {
+        const matrix& in = input_at(i);
+        if (in.tape) {
+            if (in.tape->invalidate_pass(current_pass_id)) inv = true;
+            if (in.tape->version > version) inv = true;
+            nv = std::max(nv, in.tape->version);
+        } else if (in.storage) {
+            if (in.storage->leaf_version > version) inv = true;
+            nv = std::max(nv, in.storage->leaf_version);
+        }
+    }
+    if (inv) {
+        evaluated = false;
+        version = nv;
+    }
+    return inv;
 }
 
 void* matrix::device_ptr() const { return dptr(*this); }
@@ -252,8 +324,10 @@ namespace {
 struct ViewPrim : Primitive {
     enum Kind { Transpose, Reshape, Broadcast } kind;
     matrix in;
-    std::vector<size_m> perm;
-    ViewPrim(Kind k, matrix x, std::vector<size_m> p = {}) : kind(k), in(std::move(x)), perm(std::move(p)) {}
+    std::vector<size_m> perm;          // Transpose: the axis order
+    std::vector<size_m> out_shape;     // Reshape / Broadcast: the view's shape
+    ViewPrim(Kind k, matrix x, std::vector<size_m> p = {}, std::vector<size_m> os = {})
+        : kind(k), in(std::move(x)), perm(std::move(p)), out_shape(std::move(os)) {}
     const char* name() const override { return kind == Transpose ? "Transpose" : kind == Reshape ? "Reshape" : "Broadcast"; }
     uint32_t num_inputs() const override { return 1; }
     matrix& input_at(uint32_t) override { return in; }
@@ -268,6 +342,12 @@ struct ViewPrim : Primitive {
         }
         if (kind == Reshape) return {g.reshape(in.shape_vec())};
         return {g.unbroadcast_shape(in.shape(), (int)in.dims)};
+    }
+    // primitives.cpp:3784 (transpose), :3451 (reshape), :3246 (broadcast)
+    matrix jvp(std::vector<matrix>& t) override {
+        if (kind == Transpose) return t[0].transpose(perm);
+        if (kind == Reshape) return t[0].reshape(out_shape);
+        return t[0].broadcast_to(out_shape);
     }
 };
 
@@ -334,6 +414,11 @@ struct MaxGradPrim : Primitive {
         matrix mb = matrix::equal(b, op == MX_OP_MAX ? matrix::max(a, b) : matrix::min(a, b));
         matrix mask = side ? mb : 1.0f - mb;
         return {a.zeros(), b.zeros(), gg * mask};
+    }
+    // the mask is piecewise constant in a and b: only g's tangent passes
+    matrix jvp(std::vector<matrix>& t) override {
+        matrix mb = matrix::equal(b, op == MX_OP_MAX ? matrix::max(a, b) : matrix::min(a, b));
+        return t[2] * (side ? mb : 1.0f - mb);
     }
 };
 
@@ -421,7 +506,35 @@ struct BinaryPrim : Primitive {
         default: return {a.zeros(), b.zeros()};
         }
     }
+    // primitives.cpp:496 (add), :653 (sub), :815 (mul), :975 (div), :2344 (equal), :2610 / :2765
+    // (max / min: ties to b)
+    matrix jvp(std::vector<matrix>& t) override {
+        switch (op) {
+        case MX_OP_ADD: return t[0] + t[1];
+        case MX_OP_SUB: return t[0] - t[1];
+        case MX_OP_MUL: return b * t[0] + a * t[1];
+        case MX_OP_DIV: return (b * t[0] - a * t[1]) / (b * b);
+        case MX_OP_MAX:
+        case MX_OP_MIN: {
+            matrix mask_b = matrix::equal(b, op == MX_OP_MAX ? matrix::max(a, b) : matrix::min(a, b));
+            return t[0] * (1.0f - mask_b) + t[1] * mask_b;
+        }
+        default: {
+            uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
+            check(mx_broadcast_shapes(a.shape(), a.strides(), a.dims, b.shape(), b.strides(), b.dims, os, ost, b1s, b1t,
+                                      b2s, b2t), "broadcast");
+            return matrix::zeros(std::vector<size_m>(os, os + std::max(a.dims, b.dims)), a.type);
+        }
+        }
+    }
 };
+
+// Where an axis max / min came from (primitives.cpp:1962-1965): 1/k at each of the k elements
+// equal to the extremum (given with keepdims, so it broadcasts back along the axis), 0 elsewhere.
+matrix extremum_weights(const matrix& input, const matrix& extremum, int axis) {
+    matrix mask = matrix::equal(input, extremum);
+    return mask / mask.sum(axis, true);
+}
 
 // One-axis reduction.
 struct ReducePrim : Primitive {
@@ -478,10 +591,26 @@ struct ReducePrim : Primitive {
         check(mx_launch_reduce(op, (int)in.type, rstride, n, (int)cd, cs, sOut, sIn, dptr(out), dptr(in), ws.p, ws.bytes,
                                stream), std::string("launch ") + name());
     }
+    // Sum: primitives.cpp:2904-2910; Max / Min: the gradient split evenly between the elements
+    // equal to the extremum (primitives.cpp:2044-2048, 2185-2189); ArgMax / ArgMin have none.
     std::vector<matrix> vjp(matrix& g) override {
-        if (op != MX_RED_SUM) throw std::logic_error(std::string("matrix: no vjp for ") + name());
         matrix gg = keepdims ? g : g.unsqueeze(axis);
-        return {gg.broadcast_to(in.shape_vec())};
+        if (op == MX_RED_SUM) return {gg.broadcast_to(in.shape_vec())};
+        if (op == MX_RED_MAX) return {extremum_weights(in, in.max(axis, true), axis) * gg};
+        if (op == MX_RED_MIN) return {extremum_weights(in, in.min(axis, true), axis) * gg};
+        throw std::logic_error(std::string("matrix: no vjp for ") + name());
+    }
+    // primitives.cpp:2912 (sum), :2051 / :2192 (max / min); an index has a zero tangent
+    matrix jvp(std::vector<matrix>& t) override {
+        if (op == MX_RED_SUM) return t[0].sum(axis, keepdims);
+        if (op == MX_RED_MAX) return (extremum_weights(in, in.max(axis, true), axis) * t[0]).sum(axis, keepdims);
+        if (op == MX_RED_MIN) return (extremum_weights(in, in.min(axis, true), axis) * t[0]).sum(axis, keepdims);
+        std::vector<size_m> shape;
+        for (uint32_t i = 0; i < in.dims; i++) {
+            if ((int)i == axis) { if (keepdims) shape.push_back(1); }
+            else shape.push_back(in.shape()[i]);
+        }
+        return matrix::zeros(shape, dtype::Int32);
     }
 };
 
@@ -538,6 +667,8 @@ struct DotPrim : Primitive {
         matrix gb = g.transpose(axes).dot(a, false);
         return {ga.unbroadcast_shape(a.shape(), a.dims), gb.unbroadcast_shape(bt.shape(), bt.dims)};
     }
+    // primitives.cpp:5567: bilinear, with Bt already transposed
+    matrix jvp(std::vector<matrix>& t) override { return t[0].dot(bt, true) + a.dot(t[1], true); }
 };
 
 // Max|Min(Add(Dot(...), bias), s) with bias and s leaves: the Dot launches all three (bias a row
@@ -572,9 +703,10 @@ void BinaryPrim::try_fuse_epilogue(const matrix& out) {
 // Strided copy with cast into a contiguous output.
 struct CopyPrim : Primitive {
     matrix in;
+    dtype to;
     uint32_t cd = 0;
     uint32_t cs[MX_MAX_DIMS], sD[MX_MAX_DIMS], sS[MX_MAX_DIMS];
-    explicit CopyPrim(matrix x) : in(std::move(x)) {}
+    CopyPrim(matrix x, dtype t) : in(std::move(x)), to(t) {}
     const char* name() const override { return "AsType"; }
     uint32_t num_inputs() const override { return 1; }
     matrix& input_at(uint32_t) override { return in; }
@@ -589,21 +721,22 @@ struct CopyPrim : Primitive {
               "launch AsType");
     }
     std::vector<matrix> vjp(matrix& g) override { return {g.astype(in.type)}; }
+    matrix jvp(std::vector<matrix>& t) override { return t[0].astype(to); }      // primitives.cpp:3588
 };
 
 // Channels-last convolution.
 struct ConvPrim : Primitive {
     matrix in, k;
-    std::vector<int> stride, pad_lo, dil, dil_lhs;
+    std::vector<int> stride, pad_lo, pad_hi, dil, dil_lhs;
     int groups;
     bool flip;
     std::vector<uint32_t> ishape, kshape, oshape, ist, kst, ost;
     DevBuf ws;
     size_t ws_bytes = 0;
-    ConvPrim(matrix x, matrix w, std::vector<int> s, std::vector<int> pl, std::vector<int> d, std::vector<int> dl, int g,
-             bool f)
-        : in(std::move(x)), k(std::move(w)), stride(std::move(s)), pad_lo(std::move(pl)), dil(std::move(d)),
-          dil_lhs(std::move(dl)), groups(g), flip(f) {}
+    ConvPrim(matrix x, matrix w, std::vector<int> s, std::vector<int> pl, std::vector<int> ph, std::vector<int> d,
+             std::vector<int> dl, int g, bool f)
+        : in(std::move(x)), k(std::move(w)), stride(std::move(s)), pad_lo(std::move(pl)), pad_hi(std::move(ph)),
+          dil(std::move(d)), dil_lhs(std::move(dl)), groups(g), flip(f) {}
     const char* name() const override { return "Convolve"; }
     uint32_t num_inputs() const override { return 2; }
     matrix& input_at(uint32_t i) override { return i ? k : in; }
@@ -621,6 +754,11 @@ struct ConvPrim : Primitive {
               "launch Convolve");
     }
     std::vector<matrix> vjp(matrix&) override { throw std::logic_error("matrix: no vjp for Convolve"); }
+    // primitives.cpp:298: bilinear, conv(dx, w) + conv(x, dw)
+    matrix jvp(std::vector<matrix>& t) override {
+        return matrix::conv(t[0], k, stride, pad_lo, pad_hi, dil, dil_lhs, groups, flip) +
+               matrix::conv(in, t[1], stride, pad_lo, pad_hi, dil, dil_lhs, groups, flip);
+    }
 };
 
 // The operands are cast to their promoted dtype first, as operator+ does (Matrix.mm:8312-8315).
@@ -670,7 +808,7 @@ matrix matrix::reshape(const std::vector<size_m>& new_shape) const {
     if (prod(new_shape) != prod(shp_)) throw std::invalid_argument("matrix::reshape: element count changes");
     if (!is_contiguous()) return astype(type, true).reshape(new_shape);
     return make_view(*this, new_shape, contiguous_strides(new_shape), offset,
-                     std::make_shared<ViewPrim>(ViewPrim::Reshape, *this));
+                     std::make_shared<ViewPrim>(ViewPrim::Reshape, *this, std::vector<size_m>{}, new_shape));
 }
 
 matrix matrix::flatten(int start, int end) const {
@@ -694,7 +832,7 @@ matrix matrix::unsqueeze(int axis) const {
     const size_m stride = axis < (int)dims ? str_[axis] * shp_[axis] : 1;
     s.insert(s.begin() + axis, 1);
     st.insert(st.begin() + axis, stride);
-    return make_view(*this, s, st, offset, std::make_shared<ViewPrim>(ViewPrim::Reshape, *this));
+    return make_view(*this, s, st, offset, std::make_shared<ViewPrim>(ViewPrim::Reshape, *this, std::vector<size_m>{}, s));
 }
 
 matrix matrix::broadcast_to(const std::vector<size_m>& shape) const {
@@ -706,12 +844,13 @@ matrix matrix::broadcast_to(const std::vector<size_m>& shape) const {
         else if (shp_[i] == 1) st[lead + i] = 0;
         else throw std::invalid_argument("MatrixH: Incompatible shapes for broadcasting");
     }
-    return make_view(*this, shape, st, offset, std::make_shared<ViewPrim>(ViewPrim::Broadcast, *this));
+    return make_view(*this, shape, st, offset,
+                     std::make_shared<ViewPrim>(ViewPrim::Broadcast, *this, std::vector<size_m>{}, shape));
 }
 
 matrix matrix::astype(dtype t, bool make_contig) const {
     if (t == type && (!make_contig || is_contiguous())) return *this;
-    return make_node(shp_, t, std::make_shared<CopyPrim>(*this));
+    return make_node(shp_, t, std::make_shared<CopyPrim>(*this, t));
 }
 
 // ------------------------------------------------------------------ ops
@@ -808,7 +947,7 @@ matrix matrix::conv(const matrix& input, const matrix& kernel, const std::vector
         out.push_back((size_m)(span / stride[d] + 1));
     }
     out.push_back(kernel.shape()[0]);
-    return make_node(out, input.type, std::make_shared<ConvPrim>(input, kernel, stride, pad_lo, kernel_dilation,
+    return make_node(out, input.type, std::make_shared<ConvPrim>(input, kernel, stride, pad_lo, pad_hi, kernel_dilation,
                                                                  input_dilation, groups, flip));
 }
 
@@ -825,7 +964,7 @@ namespace {
 void compile_node(const matrix& m, std::unordered_set<const Primitive*>& seen) {
     if (!m.storage) throw std::invalid_argument("matrix: empty handle in the graph");
     if (!m.tape) {                                  // leaf: device copy of the host values
-        if (!m.storage->dev || m.storage->dev_stale) m.storage->upload();
+        if (!m.storage->borrowed && (!m.storage->dev || m.storage->dev_stale)) m.storage->upload();
         return;
     }
     if (!seen.insert(m.tape.get()).second) return;
@@ -1152,13 +1291,17 @@ void run_schedule(const Schedule& sc, Executor& ex) {
             if (sc.group_of[i] >= 0) {                   // the whole group, then skip its members
                 const auto& g = sc.groups[sc.group_of[i]];
                 launch_group(g, nodes, p->stream);
-                for (int m : g) nodes[m].tape->evaluated = true;
+                for (int m : g) {
+                    nodes[m].tape->evaluated = true;
+                    nodes[m].storage->dev_version++;
+                }
                 oi += g.size() - 1;
                 continue;
             }
             p->execute(nodes[i]);
         }
         p->evaluated = true;
+        nodes[i].storage->dev_version++;
     }
     void* s0 = ex.stream(0);
     int nev = 0;
@@ -1219,8 +1362,11 @@ std::vector<uint8_t> matrix::to_host_bytes() const {
         if (!tape->evaluated) { matrix self = *this; self.eval(); }
         full.resize(storage->bytes);
         if (storage->bytes) check(mx_hip_d2h(full.data(), storage->dev, storage->bytes, nullptr), "device-to-host copy");
-    } else {
+    } else if (storage->host_is_source) {
         full = storage->host;
+    } else {                                            // a leaf whose values are on the device
+        full.resize(storage->bytes);
+        if (storage->bytes) check(mx_hip_d2h(full.data(), storage->dev, storage->bytes, nullptr), "device-to-host copy");
     }
     const size_t n = total_size();
     std::vector<uint8_t> out(n * es);
@@ -1318,4 +1464,182 @@ std::function<std::pair<matrix, std::vector<matrix>>(const std::vector<matrix>&)
 std::function<std::vector<matrix>(const std::vector<matrix>&)> matrix::grad(std::function<matrix(std::vector<matrix>)> fn) {
     auto vg = value_and_grad(std::move(fn));
     return [vg](const std::vector<matrix>& params) { return vg(params).second; };
+}
+
+std::function<std::pair<matrix, matrix>(const matrix&)> matrix::value_and_grad(std::function<matrix(matrix)> fn) {
+    auto vg = value_and_grad(std::function<matrix(std::vector<matrix>)>([fn](std::vector<matrix> p) { return fn(p[0]); }));
+    return [vg](const matrix& x) {
+        auto r = vg({x});
+        return std::make_pair(r.first, r.second[0]);
+    };
+}
+
+std::function<matrix(const matrix&)> matrix::grad(std::function<matrix(matrix)> fn) {
+    auto vg = value_and_grad(std::move(fn));
+    return [vg](const matrix& x) { return vg(x).second; };
+}
+
+// ------------------------------------------------------------------ forward mode
+std::vector<matrix> matrix::build_jvp_graph(std::vector<matrix>& output_nodes, std::vector<matrix>& input_nodes,
+                                            std::vector<matrix>& input_tangents) {
+    if (input_nodes.size() != input_tangents.size())
+        throw std::invalid_argument("matrix::build_jvp_graph: one tangent per input");
+    std::unordered_map<const void*, matrix> tan;
+    for (size_t i = 0; i < input_nodes.size(); i++) {
+        if (input_tangents[i].shape_vec() != input_nodes[i].shape_vec())
+            throw std::invalid_argument("matrix::build_jvp_graph: a tangent's shape differs from its input's");
+        tan.insert({node_id(input_nodes[i]), input_tangents[i]});
+    }
+    // the nodes that depend on an input, in topological order
+    std::unordered_map<const void*, bool> depends;
+    std::vector<const matrix*> topo;
+    std::function<void(const matrix&)> dfs = [&](const matrix& m) {
+        const void* id = node_id(m);
+        if (depends.count(id)) return;
+        bool dep = tan.count(id) > 0;
+        if (m.tape && !dep)
+            for (uint32_t i = 0; i < m.tape->num_inputs(); i++) {
+                const matrix& in = m.tape->input_at(i);
+                dfs(in);
+                if (depends[node_id(in)]) dep = true;
+            }
+        depends[id] = dep;
+        if (dep && !tan.count(id)) topo.push_back(&m);
+    };
+    for (auto& o : output_nodes) dfs(o);
+    for (const matrix* m : topo) {
+        std::vector<matrix> ts;
+        for (uint32_t i = 0; i < m->tape->num_inputs(); i++) {
+            const matrix& in = m->tape->input_at(i);
+            auto it = tan.find(node_id(in));
+            ts.push_back(it != tan.end() ? it->second : in.zeros());
+        }
+        tan.insert({node_id(*m), m->tape->jvp(ts)});
+    }
+    std::vector<matrix> out;
+    for (auto& o : output_nodes) {
+        auto it = tan.find(node_id(o));
+        out.push_back(it != tan.end() ? it->second : o.zeros());
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ compiled sub-graphs
+namespace {
+
+// A graph traced once on placeholder leaves and compiled; each CompiledNodePrim runs it on its
+// own inputs.  The placeholders borrow the inputs' device buffers for the run (no copy), and the
+// nodes of every call share the graph's output buffers (MultiInputCompilePrimitive /
+// CompiledNodePrimitive, primitives.cpp:3844-4200).
+struct CompiledGraph {
+    std::vector<matrix> samples, outputs;
+    std::vector<matrix> order;              // the graph's nodes, inputs first
+    std::vector<matrix> leaves;             // its other leaves (uploaded again when written)
+};
+
+std::shared_ptr<CompiledGraph> compile_subgraph(const std::vector<matrix>& sample_inputs,
+                                                const std::function<std::vector<matrix>(std::vector<matrix>)>& build) {
+    auto g = std::make_shared<CompiledGraph>();
+    for (const matrix& s : sample_inputs) {
+        if (!s.storage) throw std::invalid_argument("matrix::jit_graph_gpu: empty sample");
+        matrix ph = matrix::leaf(s.shape_vec(), s.type);
+        ph.storage->host.clear();
+        ph.storage->host.shrink_to_fit();
+        ph.storage->host_is_source = false;
+        ph.storage->borrowed = true;
+        ph.storage->dev_stale = false;
+        g->samples.push_back(ph);
+    }
+    g->outputs = build(g->samples);
+    for (const matrix& o : g->outputs)
+        if (!o.tape) throw std::invalid_argument("matrix::jit_graph_gpu: an output is a leaf, not a computed node");
+    matrix::compile_gpu(g->outputs);
+    Walk w;
+    for (auto& o : g->outputs) collect(o, w);
+    g->order = std::move(w.nodes);
+    for (auto& l : w.leaves)
+        if (!l.storage->borrowed) g->leaves.push_back(l);
+    return g;
+}
+
+struct CompiledNodePrim : Primitive {
+    std::shared_ptr<CompiledGraph> graph;
+    std::vector<matrix> ins;
+    CompiledNodePrim(std::shared_ptr<CompiledGraph> g, std::vector<matrix> x) : graph(std::move(g)), ins(std::move(x)) {}
+    const char* name() const override { return "CompiledGraph"; }
+    uint32_t num_inputs() const override { return (uint32_t)ins.size(); }
+    matrix& input_at(uint32_t i) override { return ins[i]; }
+    void compile(const matrix&) override {}
+    // One call's outputs are views sharing this node, so an execute runs it once for all of them.
+    // Calls of one compiled graph share its output buffers: the last call run wins (as in the
+    // reference).
+    void execute(const matrix&) override {
+        CompiledGraph& g = *graph;
+        for (size_t i = 0; i < ins.size(); i++) g.samples[i].storage->dev = dptr(ins[i]);
+        for (const matrix& l : g.leaves)
+            if (l.storage->dev_stale) l.storage->upload();
+        for (const matrix& n : g.order) {
+            Primitive* p = n.tape.get();
+            if (!p->is_view()) {
+                p->stream = stream;
+                p->execute(n);
+            }
+            p->evaluated = true;
+            n.storage->dev_version++;
+        }
+    }
+    std::vector<matrix> vjp(matrix&) override { throw std::logic_error("matrix: no vjp through a compiled graph"); }
+    matrix jvp(std::vector<matrix>&) override { throw std::logic_error("matrix: no jvp through a compiled graph"); }
+};
+
+// The lazy nodes of one call: the inputs cast / packed to the placeholders' dtype and layout when
+// they differ, one node per output sharing the output's buffer.
+std::vector<matrix> call_subgraph(const std::shared_ptr<CompiledGraph>& g, const std::vector<matrix>& inputs) {
+    if (inputs.size() != g->samples.size())
+        throw std::invalid_argument("matrix: a compiled graph takes " + std::to_string(g->samples.size()) + " inputs, " +
+                                    std::to_string(inputs.size()) + " given");
+    std::vector<matrix> ins;
+    for (size_t i = 0; i < inputs.size(); i++) {
+        const matrix& x = inputs[i];
+        const matrix& ph = g->samples[i];
+        if (!x.storage || x.shape_vec() != ph.shape_vec())
+            throw std::invalid_argument("matrix: a compiled graph's input shape differs from its sample's");
+        const bool ok = x.type == ph.type && x.is_contiguous();
+        ins.push_back(ok ? x : x.astype(ph.type, true));
+    }
+    auto prim = std::make_shared<CompiledNodePrim>(g, ins);
+    std::vector<matrix> outs;
+    for (const matrix& o : g->outputs)
+        outs.push_back(matrix::make_view(o, o.shape_vec(), o.strides_vec(), o.offset, prim));
+    return outs;
+}
+
+}  // namespace
+
+std::function<matrix(const matrix&)> matrix::jit_graph_gpu(std::function<matrix(matrix)> func, matrix sample) {
+    auto g = compile_subgraph({sample}, [&](std::vector<matrix> s) { return std::vector<matrix>{func(s[0])}; });
+    return [g](const matrix& x) { return call_subgraph(g, {x})[0]; };
+}
+
+std::function<matrix(matrix)> matrix::grad_graph_gpu(std::function<matrix(matrix)> func, matrix sample) {
+    auto g = compile_subgraph({sample}, [&](std::vector<matrix> s) {
+        matrix out = func(s[0]);
+        return std::vector<matrix>{build_grad_graph(out, s[0])};
+    });
+    return [g](matrix x) { return call_subgraph(g, {x})[0]; };
+}
+
+std::function<std::vector<matrix>(const std::vector<matrix>&)> matrix::multi_jit_graph_gpu(
+    std::function<std::vector<matrix>(std::vector<matrix>)> func, const std::vector<matrix>& sample_inputs) {
+    auto g = compile_subgraph(sample_inputs, func);
+    return [g](const std::vector<matrix>& xs) { return call_subgraph(g, xs); };
+}
+
+std::function<std::vector<matrix>(std::vector<matrix>)> matrix::grad_graph_gpu(
+    std::function<std::vector<matrix>(std::vector<matrix>)> func, const std::vector<matrix>& sample_inputs) {
+    auto g = compile_subgraph(sample_inputs, [&](std::vector<matrix> s) {
+        std::vector<matrix> outs = func(s);
+        return build_grad_graph(outs, s);
+    });
+    return [g](std::vector<matrix> xs) { return call_subgraph(g, xs); };
 }

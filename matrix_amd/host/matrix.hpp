@@ -65,6 +65,8 @@ template <typename T> constexpr dtype dtype_of() {
     else if constexpr (std::is_same_v<T, bool>) return dtype::Bool;
     else if constexpr (std::is_same_v<T, double>) return dtype::Float;
     else if constexpr (std::is_same_v<T, int>) return dtype::Int32;
+    else if constexpr (std::is_same_v<T, _Float16>) return dtype::Float16;
+    else if constexpr (std::is_same_v<T, __bf16>) return dtype::BFloat16;
     else static_assert(sizeof(T) == 0, "no dtype for this C++ type");
 }
 
@@ -73,9 +75,13 @@ namespace matrix_amd {
 struct Storage {
     size_t bytes = 0;
     void* dev = nullptr;
-    std::vector<uint8_t> host;        // a leaf's values (host side)
+    std::vector<uint8_t> host;        // a leaf's values (host side); a node's at() cache
     bool host_is_source = false;      // leaf: host holds the values, device gets a copy
     bool dev_stale = true;            // host changed since the last upload
+    bool borrowed = false;            // dev points into another allocation (a compiled graph's input)
+    uint64_t dev_version = 0;         // bumped by every execute that writes the device copy
+    uint64_t leaf_version = 0;        // a leaf's version: the epoch of its last mark_changed()
+    uint64_t host_version = ~0ull;    // dev_version the host cache of a node holds
     ~Storage();
     void allocate();                  // device memory of `bytes` (once)
     void upload();                    // host -> device, synchronous
@@ -118,8 +124,10 @@ public:
         return from_bytes(shape, type, data.data());
     }
     // A rank-0 matrix holding val converted to type (matrix.h:648-660: static_cast, the 16-bit
-    // floats rounded to nearest even).
-    template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T>>>
+    // floats rounded to nearest even).  The 16-bit float types are listed on their own: the
+    // standard library does not count them as arithmetic.
+    template <typename T, typename = std::enable_if_t<std::is_arithmetic_v<T> || std::is_same_v<T, _Float16> ||
+                                                      std::is_same_v<T, __bf16>>>
     static matrix scalar(T val, dtype type = dtype_of<T>()) {
         matrix m = leaf({}, type);
         store_scalar(type, val, m.host_data());
@@ -132,6 +140,14 @@ public:
     matrix ones() const { return ones(shp_, type); }
     void* host_data();               // a leaf's host values (write, then mark_changed())
     void mark_changed();
+    // A one-element leaf holding value (matrix.h:917): the tracked scalar a caller writes into
+    // (host_data / at), then mark_changed(), and the next execute sees it.
+    static matrix leaf_scalar(float value, dtype type = dtype::Float);
+    // Evaluate, then keep the values and drop the graph: the matrix becomes a leaf whose data stay
+    // on the device (make_leaf, Matrix.mm:2686-2691; releaseTape drops the graph of an evaluated
+    // node the same way).
+    void make_leaf();
+    void releaseTape();
 
     // ---- views and casts
     matrix transpose(const std::vector<size_m>& order) const;
@@ -189,14 +205,65 @@ public:
         return out;
     }
 
+    // The reference's names for the same cycle (Matrix.mm:8436-8469): compile_metal allocates,
+    // execute_metal launches and waits, eval_metal does both.  The device is the MI355X.
+    void compile_metal() { compile_gpu(); }
+    void execute_metal() { execute_gpu(); }
+    void eval_metal() { eval(); }
+    // Several at once (matrix.h:1722-1729): each argument a matrix or a std::vector<matrix>; one
+    // execute for all of them.  detach drops each one's graph and keeps its data.
+    template <typename... Args> static void eval(Args&... args) {
+        std::vector<matrix> all;
+        (gather(all, args), ...);
+        eval(all);
+    }
+    template <typename... Args> static void detach(Args&... args) { (detach_each(args), ...); }
+    // Element access (matrix.h:1734-1764): evaluates when needed, checks the rank, the dtype and
+    // every index, and returns a reference to the element in a host copy of the values (a leaf's
+    // own host values: write through it, then mark_changed(), as the reference requires).
+    template <typename T, typename... Args> T& at(Args... args) {
+        constexpr size_t N = sizeof...(args);
+        if (dims != N) throw std::runtime_error("Matrix rank mismatch in at().");
+        if (type != dtype_of<T>()) throw std::runtime_error("Type mismatch in at().");
+        size_t off = offset;
+        if constexpr (N > 0) {
+            const size_m idx[N] = {static_cast<size_m>(args)...};
+            for (size_t d = 0; d < N; ++d) {
+                if (idx[d] >= shp_[d])
+                    throw std::out_of_range("at(): index " + std::to_string(idx[d]) + " out of bounds for dimension " +
+                                            std::to_string(d) + " with shape " + std::to_string(shp_[d]));
+                off += (size_t)idx[d] * str_[d];
+            }
+        }
+        return reinterpret_cast<T*>(host_view())[off];
+    }
+
     // ---- autodiff
     static std::vector<matrix> build_grad_graph(std::vector<matrix>& output_nodes,
                                                 std::vector<matrix>& sample_input_nodes);
     static matrix build_grad_graph(matrix& output_node, matrix& sample_input_node);
     static std::function<std::pair<matrix, std::vector<matrix>>(const std::vector<matrix>&)> value_and_grad(
         std::function<matrix(std::vector<matrix>)> fn);
+    static std::function<std::pair<matrix, matrix>(const matrix&)> value_and_grad(std::function<matrix(matrix)> fn);
     static std::function<std::vector<matrix>(const std::vector<matrix>&)> grad(
         std::function<matrix(std::vector<matrix>)> fn);
+    static std::function<matrix(const matrix&)> grad(std::function<matrix(matrix)> fn);
+    // Forward mode (no counterpart in the reference, which has the per-node jvp only,
+    // primitives.cpp:110): the tangent of every output for the given tangents of the inputs, built
+    // from each node's jvp in topological order (inputs without a tangent contribute zero).
+    static std::vector<matrix> build_jvp_graph(std::vector<matrix>& output_nodes, std::vector<matrix>& input_nodes,
+                                               std::vector<matrix>& input_tangents);
+
+    // ---- compiled sub-graphs (Matrix.mm:1076-1175, 1413-1470): func is traced once on a leaf of
+    // the sample's shape and dtype and compiled; each call of the returned function gives lazy
+    // nodes that run the compiled graph on the call's inputs (no copy of them: the graph reads
+    // their buffers) and share its output buffers, as the reference's do.
+    static std::function<matrix(const matrix&)> jit_graph_gpu(std::function<matrix(matrix)> func, matrix sample);
+    static std::function<matrix(matrix)> grad_graph_gpu(std::function<matrix(matrix)> func, matrix sample);
+    static std::function<std::vector<matrix>(const std::vector<matrix>&)> multi_jit_graph_gpu(
+        std::function<std::vector<matrix>(std::vector<matrix>)> func, const std::vector<matrix>& sample_inputs);
+    static std::function<std::vector<matrix>(std::vector<matrix>)> grad_graph_gpu(
+        std::function<std::vector<matrix>(std::vector<matrix>)> func, const std::vector<matrix>& sample_inputs);
 
     // (internal) a node's output handle
     static matrix make_node(std::vector<size_m> shape, dtype type, std::shared_ptr<Primitive> prim);
@@ -207,6 +274,11 @@ public:
 private:
     std::vector<size_m> shp_, str_;
     friend class Primitive;
+    void* host_view();                 // host copy of the storage (evaluates, downloads when stale)
+    static void gather(std::vector<matrix>& all, matrix& m) { all.push_back(m); }
+    static void gather(std::vector<matrix>& all, std::vector<matrix>& ms) { all.insert(all.end(), ms.begin(), ms.end()); }
+    static void detach_each(matrix& m) { m.releaseTape(); }
+    static void detach_each(std::vector<matrix>& ms) { for (auto& m : ms) m.releaseTape(); }
     template <typename T> static void store_scalar(dtype type, T val, void* dst);
 };
 
@@ -312,7 +384,21 @@ public:
     virtual void compile(const matrix& out) = 0;
     virtual void execute(const matrix& out) = 0;
     virtual std::vector<matrix> vjp(matrix& grad_out) = 0;
+    // The tangent of this node's output from the tangents of its inputs (primitives.cpp:110).
+    virtual matrix jvp(std::vector<matrix>& tangents) = 0;
+    // Copies of the input handles, in input_at order (primitives.cpp:112).
+    std::vector<matrix> get_inputs() {
+        std::vector<matrix> v;
+        for (uint32_t i = 0; i < num_inputs(); i++) v.push_back(input_at(i));
+        return v;
+    }
+    // Re-evaluation after leaves change (primitives.cpp:117): a node is invalidated (evaluated =
+    // false) when any input is, or when an input leaf was marked changed after this node last
+    // took its version; memoised per pass.  Returns whether the node must run again.
+    bool invalidate_pass(uint64_t current_pass_id);
     bool compiled = false;
     bool evaluated = false;
+    uint64_t version = 1;
+    uint64_t last_visited_pass_id = 0;
     void* stream = nullptr;        // the stream execute() launches on (set by the executor)
 };
