@@ -290,6 +290,44 @@ def matmul_case(mx, dt, kind, rng):
     return launch, (a, bt, desc, K, code)
 
 
+def matmul_graph_case(mx, dt, kind, rng):
+    """launch(i) of config 3's product as the graph's A.dot(B) runs it from B stored [K, N]: the
+    tile kernel reads B N-major (no copy), except for the fp32 skinny product (8 rows of A), for
+    which dot() packs B^T with the strided copy and runs the streaming kernel on it (both launches
+    timed)."""
+    code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
+    if kind == "main":
+        a = _normal(rng, [16, 2048, 2048], 1 / np.sqrt(2048), dt)
+        b = _normal(rng, [2048, 2048], 1 / np.sqrt(2048), dt)
+        M, K, N, batch, copies = 2048, 2048, 2048, 16, 1
+    else:
+        a = _normal(rng, [8, 1, 4096], 1 / 64, dt)
+        b = _normal(rng, [4096, 4096], 1 / 64, dt)
+        M, K, N, batch, copies = 1, 4096, 4096, 8, (8 if dt == "f32" else 12)
+    A = mx.DeviceBuffer.from_numpy(a)
+    Bs = [mx.DeviceBuffer.from_numpy(b) for _ in range(copies)]
+    C = mx.DeviceBuffer(batch * M * N * a.itemsize)
+    if kind == "main" or dt != "f32":
+        desc = ([batch, M, N], [M * K, K, 1], [0, 1, N], [M * N, N, 1])      # Bt = B^T as a view
+        wsb = mx.matmul_workspace_bytes(code, desc, K)
+        W = mx.DeviceBuffer(wsb) if wsb else None
+        mm = mx.prepare_batched_matmul(code, desc, K, workspace=W.ptr if W else 0, workspace_bytes=wsb)
+
+        def launch(i=0):
+            mm(C.ptr, A.ptr, Bs[i % copies].ptr)
+        launch.keep = (A, Bs, C, W)
+        return launch
+    Bt = mx.DeviceBuffer(K * N * a.itemsize)
+    desc = ([batch, M, N], [M * K, K, 1], [0, K, 1], [M * N, N, 1])
+    mm = mx.prepare_batched_matmul(code, desc, K)
+
+    def launch(i=0):
+        mx.launch_copy_strided(code, code, ([N, K], [K, 1], [1, N]), Bt.ptr, Bs[i % copies].ptr)
+        mm(C.ptr, A.ptr, Bt.ptr)
+    launch.keep = (A, Bs, C, Bt)
+    return launch
+
+
 def config_matmul(mx):
     """Config 3: A[16,2048,2048] x B[2048,2048] (B broadcast over the batch), f32 and f16 with
     fp32 accumulation; skinny A[8,1,4096] x B[4096,4096].  B^T is packed once (dot's copy) and
@@ -311,6 +349,21 @@ def config_matmul(mx):
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[f"skinny_{dt}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         cpu_in[f"skinny_{dt}"] = host
+        del launch
+        # the same products as the graph's A.dot(B) runs them from B stored [K, N]
+        launch = matmul_graph_case(mx, dt, "main", rng)
+        ms = _timed(mx, launch, 5 if dt == "f32" else 20)
+        tf = 274_877_906_944 / (ms * 1e-3) / 1e12
+        res[f"main_{dt}_dot"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4),
+                                 "note": "B stored [K, N], read N-major by the tile kernel (no transposed copy)"}
+        del launch
+        launch = matmul_graph_case(mx, dt, "skinny", rng)
+        ms = _timed(mx, launch, 40)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[f"skinny_{dt}_dot"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                   "note": ("B stored [K, N]: the B^T copy plus the streaming kernel" if dt == "f32" else
+                                            "B stored [K, N], read N-major by the tile kernel (split K)") +
+                                           "; GB/s over the product's A + B + C bytes"}
         del launch
     res["_cpu_inputs"] = cpu_in
     return res

@@ -417,17 +417,16 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
                              if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
                          return true;
                      }();
-    // fp32 B given N-major (Bt's K stride is B's row stride, its N stride 1): the tile kernel's
-    // N-major B slot, so dot() needs no transposed copy of B
-    bool nn = false;
-    if constexpr (DT == MX_FLOAT32)
-        nn = !vec && g.ka == 1 && g.ldb == 1 && g.kb % 4 == 0 && g.N % 4 == 0 && g.lda % 4 == 0 &&
-             (uint64_t)ts.bm * g.lda * 4 < (1ull << 32) && 32ull * g.kb * 4 < (1ull << 32) &&
-             (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0 && [&] {
-                 for (int d = 0; d < g.bd.n; d++)
-                     if (g.bd.sA[d] % 4 || g.bd.sB[d] % 4) return false;
-                 return true;
-             }();
+    // B given N-major (Bt's K stride is B's row stride, its N stride 1): the tile kernel's N-major
+    // B slot (fp32: 16-byte rows of 4 columns; 16-bit: transposing LDS reads), so dot() needs no
+    // transposed copy of B
+    const bool nn = !vec && g.ka == 1 && g.ldb == 1 && g.kb % CE == 0 && g.N % CE == 0 && g.lda % CE == 0 &&
+                    (uint64_t)ts.bm * g.lda * sizeof(S) < (1ull << 32) && 64ull * g.kb * sizeof(S) < (1ull << 32) &&
+                    (uintptr_t)A % 16 == 0 && (uintptr_t)Bt % 16 == 0 && [&] {
+                        for (int d = 0; d < g.bd.n; d++)
+                            if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
+                        return true;
+                    }();
     const tile::MatrixSrc::Geom geo{};
     const char* who = "mx_launch_batched_matmul";
     if (nsplit > 1 && per < 0xffffffffull) {
@@ -438,9 +437,8 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
         gp.ksplit = ksplit;
         gp.ldc = g.N;
         gp.cn = 1;
-        if constexpr (DT == MX_FLOAT32)
-            if (nn) rc = tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc, true>(ts, gp, geo, P, A, Bt, st, who, nsplit);
-        if (!nn)
+        if (nn) rc = tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc, true>(ts, gp, geo, P, A, Bt, st, who, nsplit);
+        else
             rc = vec ? tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit)
                      : tile::launch_tile_kernel<DT, false, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit);
         if (rc) return rc;
@@ -454,10 +452,9 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
         MX_HIP(hipGetLastError());
         return MX_OK;
     }
-    int rc = -1;
-    if constexpr (DT == MX_FLOAT32)
-        if (nn) rc = tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc, true>(ts, g, geo, C, A, Bt, st, who);
-    if (rc < 0)
+    int rc;
+    if (nn) rc = tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc, true>(ts, g, geo, C, A, Bt, st, who);
+    else
         rc = vec ? tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who)
                  : tile::launch_tile_kernel<DT, false, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
     return rc || !epi ? rc : launch_bias_act<DT>(g, C, *epi, st);

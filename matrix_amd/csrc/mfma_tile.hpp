@@ -327,6 +327,108 @@ __device__ __forceinline__ void store_tile_nn(char* lds, const f4v (&r)[kTailChu
     }
 }
 
+// ------------------------------------------------------------------ 16-bit B given N-major
+// B as [K, N] with N contiguous (dot()'s B without its transposed copy).  The B slot holds the
+// pair's 64 K rows of BN elements (BN * 2 bytes each); 16-byte chunk c of K row k is stored at
+// c ^ (4 (k & 3)).  A fragment (8 consecutive K of one column, as the K-major slot gives it) comes
+// from two transposing LDS reads (ds_read_b64_tr_b16).  Within each group of 16 lanes, that read
+// takes a 4 x 16 block of 16-bit elements whose row e is the four 8-byte pieces addressed by lanes
+// 4e .. 4e + 3 (lane 4e + q: columns 4q .. 4q + 3), and returns column i of the block to lane i: so
+// lane 4e + q addresses K row kb + e, columns nb + 4q .. + 3, and lane i receives rows kb .. kb + 3
+// of column nb + i.  The swizzle puts the eight 32-byte row segments two lane groups read at once
+// (K rows kb .. kb + 3, columns nb and nb + 16) in eight distinct groups of LDS banks.
+__device__ __forceinline__ int swz_nn16(int krow, int chunk) { return chunk ^ (4 * (krow & 3)); }
+
+typedef short s4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ s4v ds_read_tr16(const char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4v*)((__attribute__((address_space(3))) char*)p));
+}
+
+// The Bt fragment of lane l for MFMA column tile t, K block kb of step HALF: lane l holds column
+// n = wn * 32 WNT + 32 t + l % 32 and K offsets 16 kb + 8 (l / 32) .. + 7 of the step, as
+// read_frags gives it from a K-major slot.
+template <int BN, int HALF, typename V>
+__device__ __forceinline__ V read_b_nn16(const char* lb, int col0, int kb, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const int krow = HALF * 32 + 16 * kb + 8 * (g >> 1) + (j >> 2);
+    const int col = col0 + 16 * (g & 1) + 4 * (j & 3);
+    const int c = col >> 3, half8 = (col & 7) * 2;          // 16-byte chunk, byte offset in it
+    const s4v lo = ds_read_tr16(lb + krow * (BN * 2) + swz_nn16(krow, c) * 16 + half8);
+    const s4v hi = ds_read_tr16(lb + (krow + 4) * (BN * 2) + swz_nn16(krow + 4, c) * 16 + half8);
+    const auto v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    V out;
+    __builtin_memcpy(&out, &v, 16);
+    return out;
+}
+
+template <int DT, int TM, int WNT, int BN, int HALF>
+__device__ __forceinline__ void read_frags_nn16(Frags<DT, TM, WNT>& f, const char* la, const char* lb, int wm, int wn,
+                                                int lane) {
+    using V = std::remove_reference_t<decltype(f.b[0][0])>;
+    const int r32 = lane & 31, h = lane >> 5;
+    constexpr int C0 = HALF * STEP_CHUNKS;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+        for (int t = 0; t < TM; t++) {
+            const int ra = wm * (TM * 32) + t * 32 + r32;
+            f.a[kb][t] = *reinterpret_cast<const V*>(la + ra * ROWB + swz(ra, C0 + 2 * kb + h) * 16);
+        }
+#pragma unroll
+        for (int t = 0; t < WNT; t++) f.b[kb][t] = read_b_nn16<BN, HALF, V>(lb, wn * (WNT * 32) + t * 32, kb, lane);
+    }
+}
+
+// DMA of the 16-bit N-major B slot: one instruction fills 1 KB = 512 / BN K rows; wave w's
+// instruction i fills rows RPI (N w + i) ..; lane L lands at row RPI (N w + i) + L / (BN / 8),
+// stored chunk L % (BN / 8), so it fetches the logical chunk swz_nn16 stores there.  Columns past
+// N load the row's last whole chunk (N is a multiple of 8; those C columns are never stored).
+template <int BN, int N>
+__device__ __forceinline__ DmaOffsets<N> dma_offsets_nn16(uint32_t cols_valid, uint32_t ldk, int wave, int lane) {
+    constexpr int CPRN = BN / 8;                         // 16-byte chunks per K row
+    constexpr int RPI = 64 / CPRN;                       // K rows per DMA instruction
+    DmaOffsets<N> o;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int row = (wave * N + i) * RPI + lane / CPRN;
+        const uint32_t col = min((uint32_t)swz_nn16(row, lane % CPRN) * 8, cols_valid - 8);
+        o.v[i] = ((uint32_t)row * ldk + col) * 2u;
+    }
+    return o;
+}
+
+// One K step (32 rows) of the 16-bit N-major B tile through registers, element loads, zero past K
+// and past N, into rows 0 .. 31 of the slot.  Thread chunk q = tid + 256 j is K row q / (BN / 8),
+// logical chunk q % (BN / 8).
+template <int BN> constexpr int kTailChunksNN16 = 32 * (BN / 8) / NTHREADS;
+
+template <int BN>
+__device__ __forceinline__ void load_tile_guarded_nn16(uint4 (&r)[kTailChunksNN16<BN>], const uint16_t* __restrict__ base,
+                                                       uint32_t cols_valid, uint32_t ldk, uint32_t k0, uint32_t K) {
+#pragma unroll
+    for (int j = 0; j < kTailChunksNN16<BN>; j++) {
+        const int q = threadIdx.x + NTHREADS * j;
+        const uint32_t k = k0 + (uint32_t)(q / (BN / 8));
+        const uint32_t c = (uint32_t)(q % (BN / 8)) * 8;
+        uint16_t tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) tmp[e] = (k < K && c + e < cols_valid) ? base[(uint64_t)k * ldk + c + e] : 0;
+        __builtin_memcpy(&r[j], tmp, 16);
+    }
+}
+
+template <int BN>
+__device__ __forceinline__ void store_tile_nn16(char* lds, const uint4 (&r)[kTailChunksNN16<BN>]) {
+#pragma unroll
+    for (int j = 0; j < kTailChunksNN16<BN>; j++) {
+        const int q = threadIdx.x + NTHREADS * j;
+        const int row = q / (BN / 8), c = q % (BN / 8);
+        *reinterpret_cast<uint4*>(lds + row * (BN * 2) + swz_nn16(row, c) * 16) = r[j];
+    }
+}
+
 // s_waitcnt vmcnt(N), expcnt / lgkmcnt left at their maximum (gfx9 encoding: vmcnt in bits
 // 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
 template <int N>
@@ -346,23 +448,25 @@ template <int DT> constexpr int kMfmaPerSlot = DT == MX_FLOAT32 ? 4 : 1;
 // First step of a pair: the next step's fragment reads, one after each leading MFMA slot.  The
 // pair's first MFMA goes before the first read: LDS reads complete in order, so an MFMA behind a
 // new read would wait for that read as well as for its own (long since loaded) fragments.
-template <int DT, int TM, int WNT>
+template <int DT, int TM, int WNT, int NR>
 __device__ __forceinline__ void interleave_even() {
-    constexpr int MF = kMfmaPerSlot<DT>, SLOTS = 2 * TM * WNT, NR = 2 * (TM + WNT);
-    static_assert(NR <= SLOTS, "interleave counts");
+    constexpr int MF = kMfmaPerSlot<DT>, SLOTS = 2 * TM * WNT;
+    constexpr int RPS = (NR + SLOTS - 1) / SLOTS;              // reads per slot
+    constexpr int USED = (NR + RPS - 1) / RPS;                 // slots that carry reads
+    static_assert(USED <= SLOTS, "interleave counts");
 #pragma unroll
-    for (int i = 0; i < NR; i++) {
+    for (int i = 0; i < USED; i++) {
         __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, RPS, 0);
     }
-    if constexpr (SLOTS > NR) __builtin_amdgcn_sched_group_barrier(0x008, (SLOTS - NR) * MF, 0);
+    if constexpr (SLOTS > USED) __builtin_amdgcn_sched_group_barrier(0x008, (SLOTS - USED) * MF, 0);
 }
 
 // Second step of a pair, after its barrier (TM WNT slots left): the next step's fragment reads
 // over the first half of the slots, the DMA of the pair two ahead over all of them.
-template <int DT, int TM, int WNT, int BM, int BN>
+template <int DT, int TM, int WNT, int BM, int BN, int NR>
 __device__ __forceinline__ void interleave_odd() {
-    constexpr int MF = kMfmaPerSlot<DT>, H = TM * WNT, NR = 2 * (TM + WNT), ND = kDma<BM> + kDma<BN>;
+    constexpr int MF = kMfmaPerSlot<DT>, H = TM * WNT, ND = kDma<BM> + kDma<BN>;
     constexpr int RPS = NR / (H / 2);                          // reads per slot, first half
     constexpr int D1 = (ND + H - 1) / H;                       // DMAs per slot, first half
     constexpr int D2 = (ND - D1 * (H / 2)) / (H / 2);          // DMAs per slot, second half
@@ -409,7 +513,8 @@ __device__ __forceinline__ void ring_barrier() {
 // SPLIT: the K range is cut into g.ksplit-element pieces, one per block along the outermost
 // block-batch index; the block writes its fp32 partial tile to Cv as [split][batch][M][N]
 // (g.ldc = N, g.cn = 1), and a second kernel sums the splits in order.
-// BNN (fp32 only): Bt is N-major (B as [K, N]: g.ldb == 1, g.kb is B's row stride), see FragsNN.
+// BNN: Bt is N-major (B as [K, N]: g.ldb == 1, g.kb is B's row stride); fp32 reads it as FragsNN
+// describes, 16-bit types through transposing LDS reads (read_frags_nn16).
 template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src, bool BNN = false>
 __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ Cv,
                                                              const typename MmaTraits<DT>::S* __restrict__ A,
@@ -470,7 +575,8 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave >> 1, wn = wave & 1;
 
-    static_assert(!BNN || DT == MX_FLOAT32, "the N-major B layout is fp32 only");
+    constexpr bool NN32 = BNN && DT == MX_FLOAT32;      // fp32 N-major B (FragsNN)
+    constexpr bool NN16 = BNN && DT != MX_FLOAT32;      // 16-bit N-major B (transposing reads)
     f16v acc[TM][WNT];
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -483,21 +589,26 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     const uint32_t KP = VEC ? Klen / (2 * KSTEP) : 0;  // whole K pairs copied by LDS DMA
     // Fragments are double-buffered in registers: f0 holds a pair's first step, f1 its second;
     // each step reads the next step's fragments while its own MFMAs run.
-    using FR = std::conditional_t<BNN, FragsNN<TM, WNT>, Frags<DT, TM, WNT>>;
+    using FR = std::conditional_t<NN32, FragsNN<TM, WNT>, Frags<DT, TM, WNT>>;
     FR f0, f1;
     auto read_step = [&](auto half, FR& f, const char* la, const char* lb) {
         constexpr int HALF = decltype(half)::value;
-        if constexpr (BNN) read_frags_nn<TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
+        if constexpr (NN32) read_frags_nn<TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
+        else if constexpr (NN16) read_frags_nn16<DT, TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
         else read_frags<DT, TM, WNT, HALF>(f, la, lb, wm, wn, lane);
     };
     auto mma = [&](auto i0, auto i1, const FR& f) {
         constexpr int I0_ = decltype(i0)::value, I1_ = decltype(i1)::value;
-        if constexpr (BNN) mma_step_nn<TM, WNT, I0_, I1_>(acc, f);
+        if constexpr (NN32) mma_step_nn<TM, WNT, I0_, I1_>(acc, f);
         else mma_step<DT, TM, WNT, I0_, I1_>(acc, f);
     };
+    // LDS reads per step: one 16-byte read per A fragment and per K-major B fragment, two 8-byte
+    // transposing reads per N-major one
+    constexpr int NREADS = 2 * (TM + (NN16 ? 2 : 1) * WNT);
     const auto sa = Src::template a_init<S, DMA_A>(g, geo, m0, rows_a, wave, lane);
-    const DmaOffsets<DMA_B> ob = BNN ? dma_offsets_nn<BN, DMA_B>(rows_b, g.kb, wave, lane)
-                                     : dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
+    const DmaOffsets<DMA_B> ob = NN32   ? dma_offsets_nn<BN, DMA_B>(rows_b, g.kb, wave, lane)
+                                 : NN16 ? dma_offsets_nn16<BN, DMA_B>(rows_b, g.kb, wave, lane)
+                                        : dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
     auto dma_pair = [&](auto s, uint32_t p) {
         Src::template a_dma<S, DMA_A>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
         if constexpr (BNN) dma_rows<S, DMA_B>(slot_b(s), Bblk + (uint64_t)p * 2 * KSTEP * g.kb, ob, 0, wave);
@@ -526,7 +637,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         constexpr int MF = kMfmaPerSlot<DT>;
         read_step(I1{}, f1, slot_a(s), slot_b(s));
         mma(I0{}, ITM{}, f0);
-        if constexpr (DT != MX_FLOAT32) interleave_even<DT, TM, WNT>();
+        if constexpr (DT != MX_FLOAT32) interleave_even<DT, TM, WNT, NREADS>();
         __builtin_amdgcn_sched_barrier(0);
         mma(I0{}, IH{}, f1);
         if constexpr (DT != MX_FLOAT32) __builtin_amdgcn_sched_group_barrier(0x008, TM * WNT * MF, 0);
@@ -542,7 +653,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
             read_step(I0{}, f0, slot_a(SN{}), slot_b(SN{}));
         }
         mma(IH{}, ITM{}, f1);
-        if constexpr (DT != MX_FLOAT32) interleave_odd<DT, TM, WNT, BM, BN>();
+        if constexpr (DT != MX_FLOAT32) interleave_odd<DT, TM, WNT, BM, BN, NREADS>();
         __builtin_amdgcn_sched_barrier(0);
     };
     // the last pairs: no DMA past the end, no barrier after the last
@@ -590,10 +701,14 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         for (uint32_t kt = 2 * KP; kt < KT; kt++) {
             uint4 ra[kTailChunks<BM>];
             load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
-            if constexpr (BNN) {
+            if constexpr (NN32) {
                 f4v rb[kTailChunksNN<BN>];
                 load_tile_guarded_nn<BN>(rb, reinterpret_cast<const float*>(Bblk), rows_b, g.kb, kt * KSTEP, Klen);
                 store_tile_nn<BN>(lb0, rb);
+            } else if constexpr (NN16) {
+                uint4 rb[kTailChunksNN16<BN>];
+                load_tile_guarded_nn16<BN>(rb, Bblk, rows_b, g.kb, kt * KSTEP, Klen);
+                store_tile_nn16<BN>(lb0, rb);
             } else {
                 uint4 rb[kTailChunks<BN>];
                 load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
@@ -617,7 +732,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         else return float_to_bf16(v);
     };
     const bool vec_store = g.cn == 1 && Src::template row_vec_ok<CT>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
-    if constexpr (BNN) {
+    if constexpr (NN32) {
         // accumulator q of MFMA tile (i, .) holds, in register r, C column
         // WNT (8 (r / 4) + 4 h + r % 4) + q of the wave's column range
         const uint32_t cw = n0 + wn * (WNT * 32);

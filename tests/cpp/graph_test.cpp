@@ -89,10 +89,17 @@ CASE(shapes_dot_and_conv) {
     matrix c = a.dot(b);
     EXPECT(c.dims == 3 && c.shape()[0] == 16 && c.shape()[1] == 64 && c.shape()[2] == 48, "dot shape");
     EXPECT(throws([&] { (void)a.dot(matrix::leaf({31, 48})); }), "core-dimension mismatch throws");
-    // fp32 B in its [K, N] layout reaches the GEMM as the transposed view of its own storage
+    // a float B in its [K, N] layout reaches the GEMM as the transposed view of its own storage
     EXPECT(c.tape && c.tape->input_at(1).storage == b.storage, "fp32 N-major B is not copied");
-    matrix c16 = matrix::leaf({64, 32}, dtype::Float16).dot(matrix::leaf({32, 48}, dtype::Float16));
-    EXPECT(c16.tape->input_at(1).tape && c16.tape->input_at(1).is_contiguous(), "fp16 B^T is packed");
+    for (dtype t : {dtype::Float16, dtype::BFloat16}) {
+        matrix b16 = matrix::leaf({32, 48}, t);
+        matrix c16 = matrix::leaf({64, 32}, t).dot(b16);
+        EXPECT(c16.tape->input_at(1).storage == b16.storage, "16-bit N-major B is not copied");
+        matrix c40 = matrix::leaf({64, 32}, t).dot(matrix::leaf({32, 44}, t));
+        EXPECT(c40.tape->input_at(1).is_contiguous(), "16-bit N not a multiple of 8: B^T is packed");
+    }
+    matrix cs = matrix::leaf({8, 1, 32}).dot(matrix::leaf({32, 48}));
+    EXPECT(cs.tape->input_at(1).is_contiguous(), "fp32, at most 16 rows of A (the streaming kernel): B^T is packed");
     matrix c10 = a.dot(matrix::leaf({32, 10}));
     EXPECT(c10.tape->input_at(1).is_contiguous(), "N not a multiple of 4: B^T is packed");
     matrix x = matrix::leaf({2, 56, 56, 64});

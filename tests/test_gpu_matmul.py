@@ -262,68 +262,82 @@ def test_skinny_one_hot_exact(mx, orc, M):
     assert np.array_equal(got.reshape(M, N), bt[:, ks].T)
 
 
+NN_TOL64 = {"FLOAT32": 1e-5, "FLOAT16": 2e-3, "BFLOAT16": 1e-2}   # vs fp64 of the same inputs
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
 @pytest.mark.parametrize("case", [
-    ([2, 300, 200], [2, 200, 152]),      # ragged M, K tail, N a multiple of 4 but not of the tile
+    ([2, 300, 200], [2, 200, 152]),      # ragged M, K tail, N a multiple of 8 but not of the tile
     ([512, 1024], [1024, 4096]),         # the MLP's first layer (split K)
-    ([3, 130, 96], [3, 96, 260]),        # per-batch B
+    ([3, 130, 96], [3, 96, 264]),        # per-batch B
+    ([3, 130, 96], [3, 96, 260]),        # N a multiple of 4, not 8: 16-bit takes the strided path
     ([4, 64, 128], [128, 64]),           # B shared by the batch (folds into M)
     ([100, 3000], [3000, 72]),           # long ragged K: split K, short last split
     ([64, 40], [40, 10]),                # N not a multiple of 4: the strided fallback
 ])
-def test_n_major_b(mx, orc, case):
-    """fp32 B handed over as [..., K, N] (Bt is its transposed view: N stride 1, K stride N)."""
+def test_n_major_b(mx, orc, dt, case):
+    """B handed over as [..., K, N] (Bt is its transposed view: N stride 1, K stride N): fp32 reads
+    it through 16-byte rows of 4 columns, 16-bit types through transposing LDS reads; checked
+    against the oracle on the packed Bt the reference's dot() builds, and in fp64."""
+    code = getattr(mx, dt)
     rng = np.random.default_rng(16)
     a_shape, b_shape = case
     K, N = b_shape[-2], b_shape[-1]
-    a = (rng.standard_normal(a_shape) / math.sqrt(K)).astype(np.float32)
-    b = rng.standard_normal(b_shape).astype(np.float32)
+    a = gen(rng, code, a_shape, 1.0 / math.sqrt(K), mx)
+    b = gen(rng, code, b_shape, 1.0, mx)
     bst = contiguous_strides(b_shape)
     bt_shape = b_shape[:-2] + [N, K]
     bt_strides = bst[:-2] + [1, N]
-    got, _, out = run_mm(mx, orc, mx.FLOAT32, a, b, bt_shape=bt_shape, bt_strides=bt_strides, oracle=False)
+    got, _, out = run_mm(mx, orc, code, a, b, bt_shape=bt_shape, bt_strides=bt_strides, oracle=False)
     # the oracle reads K unit-stride: it gets the packed Bt the reference's dot() would build
     bt = np.ascontiguousarray(np.swapaxes(b, -1, -2))
     _, desc = matmul_desc(mx, list(a_shape), contiguous_strides(a_shape), list(bt.shape), contiguous_strides(bt.shape))
-    ref = orc.batched_matmul(mx.FLOAT32, desc, K, a.reshape(-1), bt.reshape(-1), int(np.prod(out)), acc=orc.ACC_F32)
-    assert normwise_rel(got, ref) <= 1e-4
-    ref64 = np.matmul(a.astype(np.float64), b.astype(np.float64))
-    assert normwise_rel(got, ref64.reshape(-1)) <= 1e-5
-    got2, _, _ = run_mm(mx, orc, mx.FLOAT32, a, b, bt_shape=bt_shape, bt_strides=bt_strides, oracle=False)
+    ref = orc.batched_matmul(code, desc, K, a.reshape(-1), bt.reshape(-1), int(np.prod(out)), acc=orc.ACC_F32)
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
+    ref64 = np.matmul(as_f32(code, a, mx).astype(np.float64), as_f32(code, b, mx).astype(np.float64))
+    assert normwise_rel(as_f32(code, got, mx), ref64.reshape(-1)) <= NN_TOL64[dt]
+    got2, _, _ = run_mm(mx, orc, code, a, b, bt_shape=bt_shape, bt_strides=bt_strides, oracle=False)
     assert np.array_equal(got, got2)
 
 
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
 @pytest.mark.parametrize("case", [
     ([4096, 64], [64, 8192]),            # 256 x 256 tiles
     ([131072, 64], [64, 128]),           # 256 x 128 tiles
 ])
-def test_n_major_b_large_tiles(mx, case):
+def test_n_major_b_large_tiles(mx, dt, case):
     """The N-major B slot in the two 256-row tile shapes (checked in fp64 with numpy)."""
+    code = getattr(mx, dt)
     rng = np.random.default_rng(17)
     a_shape, b_shape = case
     K, N = b_shape
-    a = (rng.standard_normal(a_shape) / math.sqrt(K)).astype(np.float32)
-    b = rng.standard_normal(b_shape).astype(np.float32)
+    a = gen(rng, code, a_shape, 1.0 / math.sqrt(K), mx)
+    b = gen(rng, code, b_shape, 1.0, mx)
     M = a_shape[0]
     A = mx.DeviceBuffer.from_numpy(a.reshape(-1))
     B = mx.DeviceBuffer.from_numpy(b.reshape(-1))
-    C = mx.DeviceBuffer(M * N * 4)
+    C = mx.DeviceBuffer(M * N * a.itemsize)
     out, desc = matmul_desc(mx, [M, K], [K, 1], [N, K], [1, N])
-    mx.launch_batched_matmul(mx.FLOAT32, desc, K, C.ptr, A.ptr, B.ptr)
+    mx.launch_batched_matmul(code, desc, K, C.ptr, A.ptr, B.ptr)
     mx.sync()
-    got = C.download(np.float32, M * N)
-    ref64 = a.astype(np.float64) @ b.astype(np.float64)
-    assert normwise_rel(got, ref64.reshape(-1)) <= 1e-5
+    got = C.download(a.dtype, M * N)
+    ref64 = as_f32(code, a, mx).astype(np.float64) @ as_f32(code, b, mx).astype(np.float64)
+    assert normwise_rel(as_f32(code, got, mx), ref64.reshape(-1)) <= NN_TOL64[dt]
 
 
-
-@pytest.mark.parametrize("MKN", [(300, 200, 152), (1024, 256, 512)])
-def test_n_major_b_one_hot_exact(mx, orc, MKN):
-    """One-hot A rows pick B rows exactly: C[m, :] = B[k_m, :] (column placement of the epilogue)."""
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("MKN", [(300, 200, 152), (1024, 256, 512), (256, 64, 256)])
+def test_n_major_b_one_hot_exact(mx, orc, dt, MKN):
+    """One-hot A rows pick B rows exactly: C[m, :] = B[k_m, :] (the columns and K rows of the N-major
+    slot and the epilogue's placement)."""
+    code = getattr(mx, dt)
     M, K, N = MKN
     rng = np.random.default_rng(18)
     ks = rng.integers(0, K, M)
-    a = np.zeros([M, K], np.float32)
-    a[np.arange(M), ks] = 1.0
-    b = rng.standard_normal([K, N]).astype(np.float32)
-    got, _, _ = run_mm(mx, orc, mx.FLOAT32, a, b, bt_shape=[N, K], bt_strides=[1, N], oracle=False)
+    one = gen(rng, code, [1], 0.0, mx)
+    a = np.zeros([M, K], one.dtype)
+    a[np.arange(M), ks] = np.array([1.0], np.float32).astype(np.float16) if code == mx.FLOAT16 else (
+        np.float32(1.0) if code == mx.FLOAT32 else np.uint16(0x3F80))
+    b = gen(rng, code, [K, N], 1.0, mx)
+    got, _, _ = run_mm(mx, orc, code, a, b, bt_shape=[N, K], bt_strides=[1, N], oracle=False)
     assert np.array_equal(got.reshape(M, N), b[ks])
