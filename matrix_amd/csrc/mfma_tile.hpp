@@ -499,6 +499,108 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// The epilogue of the K-major / 16-bit tile kernels: acc[i][j][4 q + e] is C[row, col] with
+// row = 32 i + lane % 32 and col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
+// of the wave's (wm, wn) quarter of the tile at (m0, n0).
+// An interior tile with unit-stride 16-byte aligned C rows goes through LDS when the wave's quarter
+// fits `stage` (STAGE: 16-bit results, and fp32 128 x 128 tiles): the fragment layout would make
+// every store instruction touch 32 rows with 16 bytes each (a 256 x 2048 x 64 f16 product, one K
+// pair, took 19 us for its 32 MB of C); staged, 64 lanes store whole 16-byte chunks of consecutive
+// row bytes.  The quarter is written to LDS whole (16-byte chunk c of row r at
+// c ^ (r mod chunks per row)), then read back and stored row-major.  Otherwise an interior tile
+// stores 4 columns per instruction from the fragments, and other tiles one element at a time.
+template <int DT, int BM, int BN, bool SPLIT, class Src, bool STAGE, typename CT>
+__device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN / 64], const GemmArgs& g,
+                                        const typename Src::Geom& geo, uint32_t m0, uint32_t n0, int wm, int wn, int lane,
+                                        bool vec_store, char* stage) {
+    constexpr int TM = BM / 64, WNT = BN / 64;
+    const int h = lane >> 5, c32 = lane & 31;
+    auto cvt = [](float v) -> CT {
+        if constexpr (SPLIT || DT == MX_FLOAT32) return v;
+        else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
+        else return float_to_bf16(v);
+    };
+    const bool interior = m0 + BM <= g.M && n0 + BN <= g.N && vec_store;
+    if constexpr (STAGE) {
+        if (interior) {
+            constexpr int RB = WNT * 32 * (int)sizeof(CT);       // bytes of a staged row
+            constexpr int CPRS = RB / 16;                        // 16-byte chunks per staged row
+            constexpr int EPC = 16 / (int)sizeof(CT);            // elements per chunk
+            static_assert((CPRS & (CPRS - 1)) == 0 && CPRS <= 32, "staged row chunks");
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int r = i * 32 + c32;
+#pragma unroll
+                for (int j = 0; j < WNT; j++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int col = j * 32 + 8 * q + 4 * h;
+                        char* dst = stage + r * RB + (((col / EPC) ^ (r & (CPRS - 1))) * 16) + (col % EPC) * (int)sizeof(CT);
+                        if constexpr (sizeof(CT) == 4) {
+                            *reinterpret_cast<f4v*>(dst) = f4v{acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                               acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                        } else {
+                            uint2 v;
+                            v.x = (uint32_t)cvt(acc[i][j][4 * q]) | ((uint32_t)cvt(acc[i][j][4 * q + 1]) << 16);
+                            v.y = (uint32_t)cvt(acc[i][j][4 * q + 2]) | ((uint32_t)cvt(acc[i][j][4 * q + 3]) << 16);
+                            *reinterpret_cast<uint2*>(dst) = v;
+                        }
+                    }
+            }
+            // LDS accesses of one wave complete in order: the reads below see the writes above
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            asm volatile("" ::: "memory");
+            const uint32_t row0 = m0 + wm * (TM * 32);
+            CT* cbase = Cbat + n0 + wn * (WNT * 32);
+            constexpr int RPI = 64 / CPRS;                       // rows per store instruction
+            const int c = lane % CPRS;
+#pragma unroll 8
+            for (int it = 0; it < TM * 32 / RPI; it++) {
+                const int rr = it * RPI + lane / CPRS;
+                const uint4 v = *reinterpret_cast<const uint4*>(stage + rr * RB + ((c ^ (rr & (CPRS - 1))) * 16));
+                *reinterpret_cast<uint4*>(cbase + Src::row_off(g, geo, row0 + rr) + c * EPC) = v;
+            }
+            return;
+        }
+    }
+    if (interior) {                                           // 4 columns per store
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+            CT* crow = Cbat + Src::row_off(g, geo, row) + n0 + wn * (WNT * 32) + 4 * h;
+#pragma unroll
+            for (int j = 0; j < WNT; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    CT* p = crow + j * 32 + 8 * q;
+                    if constexpr (sizeof(CT) == 4) {
+                        *reinterpret_cast<float4*>(p) =
+                            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                    } else {
+                        uint2 v;
+                        v.x = (uint32_t)cvt(acc[i][j][4 * q]) | ((uint32_t)cvt(acc[i][j][4 * q + 1]) << 16);
+                        v.y = (uint32_t)cvt(acc[i][j][4 * q + 2]) | ((uint32_t)cvt(acc[i][j][4 * q + 3]) << 16);
+                        *reinterpret_cast<uint2*>(p) = v;
+                    }
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+        if (row >= g.M) continue;
+        CT* crow = Cbat + Src::row_off(g, geo, row);
+#pragma unroll
+        for (int j = 0; j < WNT; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t col = n0 + wn * (WNT * 32) + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
+                if (col < g.N) crow[(uint64_t)col * g.cn] = cvt(acc[i][j][r]);
+            }
+    }
+}
+
 // ------------------------------------------------------------------ the tile kernel
 // Src provides:
 //   Geom                                  extra kernel argument (empty for GEMM)
@@ -726,11 +828,6 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     // col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
     CT* Cbat = static_cast<CT*>(Cv) + offC;
     const int h = lane >> 5, c32 = lane & 31;
-    auto cvt = [](float v) -> CT {
-        if constexpr (SPLIT || DT == MX_FLOAT32) return v;
-        else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
-        else return float_to_bf16(v);
-    };
     const bool vec_store = g.cn == 1 && Src::template row_vec_ok<CT>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
     if constexpr (NN32) {
         // accumulator q of MFMA tile (i, .) holds, in register r, C column
@@ -760,42 +857,11 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         }
         return;
     }
-    if (m0 + BM <= g.M && n0 + BN <= g.N && vec_store) {   // interior tile: 4 columns per store
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
-            CT* crow = Cbat + Src::row_off(g, geo, row) + n0 + wn * (WNT * 32) + 4 * h;
-#pragma unroll
-            for (int j = 0; j < WNT; j++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    CT* p = crow + j * 32 + 8 * q;
-                    if constexpr (sizeof(CT) == 4) {
-                        *reinterpret_cast<float4*>(p) =
-                            make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-                    } else {
-                        uint2 v;
-                        v.x = (uint32_t)cvt(acc[i][j][4 * q]) | ((uint32_t)cvt(acc[i][j][4 * q + 1]) << 16);
-                        v.y = (uint32_t)cvt(acc[i][j][4 * q + 2]) | ((uint32_t)cvt(acc[i][j][4 * q + 3]) << 16);
-                        *reinterpret_cast<uint2*>(p) = v;
-                    }
-                }
-        }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
-        if (row >= g.M) continue;
-        CT* crow = Cbat + Src::row_off(g, geo, row);
-#pragma unroll
-        for (int j = 0; j < WNT; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint32_t col = n0 + wn * (WNT * 32) + j * 32 + (r >> 2) * 8 + h * 4 + (r & 3);
-                if (col < g.N) crow[(uint64_t)col * g.cn] = cvt(acc[i][j][r]);
-            }
-    }
+    // the epilogue's LDS stage: this wave's quarter of C in one of the four slot arrays (free now:
+    // every wave has passed the barrier after its last fragment reads)
+    constexpr bool STAGE = (BM / 2) * (BN / 2) * (int)sizeof(CT) <= (SLOT_A < SLOT_B ? SLOT_A : SLOT_B);
+    char* stage = wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? lb0 : lb1;
+    store_c<DT, BM, BN, SPLIT, Src, STAGE>(Cbat, acc, g, geo, m0, n0, wm, wn, lane, vec_store, stage);
 }
 
 // Tile shape for a problem: 256 x 256 tiles while they give at least one block per CU (256), 256 x
