@@ -101,7 +101,9 @@ int mx_hip_event_elapsed_ms(void* start, void* stop, float* ms);
  * max/min backends (Matrix.mm:13378-13478, Matrix.mm:14668-14783) and equal_backend
  * (Matrix.mm:14469-14540).  The arrays are exactly CollapsedDims_3 (Mods/Utils.h:142-148)
  * from collapse_dims (Mods/Utils.mm:169-202): shape, stridesC (= sR), stridesA, stridesB.
- * cdims == 0 is the rank-0 case (Matrix.mm:7460-7469).  A, B and R share one dtype. */
+ * cdims == 0 is the rank-0 case (Matrix.mm:7460-7469).  A, B and R share one dtype: any of the
+ * 12 real codes for every op; MX_COMPLEX64 for ADD / SUB / MUL / DIV only, as the reference
+ * instantiates it (BrodcastedAdd.metal:95 and siblings), else MX_ERR_UNSUPPORTED. */
 int mx_launch_bcast_binary(int op, int dtype, int cdims, const uint32_t* shape,
                            const uint32_t* sR, const uint32_t* sA, const uint32_t* sB,
                            void* R, const void* A, const void* B, void* stream);
@@ -242,7 +244,9 @@ int mx_launch_conv_nd(int dtype, int nspatial, const uint32_t* in_shape,
 
 /* dst[sum idx * sDst] = cast(src[sum idx * sSrc]) over a collapsed space.  Replaces
  * copyGPUinplace / copyGPUinplaceTypeCasted and the CopyInplaceGPU kernels
- * (Matrix.mm:1699-1976, Copy.metal:14-80). */
+ * (Matrix.mm:1699-1976, Copy.metal:14-80).  Any pair of the 12 real codes; within one dtype
+ * (MX_COMPLEX64 included) the element's bytes move unchanged; a real code -> MX_COMPLEX64 gives
+ * (float(v), 0) (complex.h:22); MX_COMPLEX64 -> a real code is MX_ERR_UNSUPPORTED. */
 int mx_launch_copy_strided(int dst_dtype, int src_dtype, int cdims, const uint32_t* shape,
                            const uint32_t* sDst, const uint32_t* sSrc,
                            void* dst, const void* src, void* stream);

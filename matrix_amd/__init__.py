@@ -36,11 +36,12 @@ MAX_DIMS = 8
 NP_DTYPE = {
     FLOAT32: np.float32, FLOAT16: np.float16, UINT8: np.uint8, INT32: np.int32, INT16: np.int16,
     UINT32: np.uint32, UINT16: np.uint16, BOOL: np.bool_, INT8: np.int8, BFLOAT16: np.uint16,
-    INT64: np.int64, UINT64: np.uint64,
+    INT64: np.int64, UINT64: np.uint64, COMPLEX64: np.complex64,
 }
 DTYPE_NAME = {
     FLOAT32: "f32", FLOAT16: "f16", UINT8: "u8", INT32: "i32", INT16: "i16", UINT32: "u32",
     UINT16: "u16", BOOL: "bool", INT8: "i8", BFLOAT16: "bf16", INT64: "i64", UINT64: "u64",
+    COMPLEX64: "c64",
 }
 
 

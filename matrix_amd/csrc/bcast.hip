@@ -7,7 +7,8 @@
 //     MIN (arm64 sdiv / udiv, the reference's platform);
 //   - Max is (a < b) ? b : a and Min is (b < a) ? b : a, selecting the operand's own bits
 //     (std::max / std::min), so NaN and signed-zero ties resolve as on the CPU;
-//   - Equal writes 1 / 0 in the operands' dtype.
+//   - Equal writes 1 / 0 in the operands' dtype;
+//   - complex64 (Add / Sub / Mul / Divide only) follows complex.h:28-52.
 //
 // Layout: the iteration space is the collapsed CollapsedDims_3 of collapse_dims
 // (Mods/Utils.mm:169-202).  When the innermost collapsed axis is unit-stride in the output
@@ -336,6 +337,17 @@ extern "C" int mx_launch_bcast_binary(int op, int dtype, int cdims, const uint32
     if (!R || !A || !B) return fail(MX_ERR_INVALID_ARG, "mx_launch_bcast_binary: null buffer");
     hipStream_t st;
     if (!resolve_stream(stream, &st)) return MX_ERR_NOT_INITIALIZED;
+    if (dtype == MX_COMPLEX64) {
+        switch (op) {
+        case MX_OP_ADD: return launch_typed<MX_COMPLEX64, MX_OP_ADD>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+        case MX_OP_SUB: return launch_typed<MX_COMPLEX64, MX_OP_SUB>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+        case MX_OP_MUL: return launch_typed<MX_COMPLEX64, MX_OP_MUL>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+        case MX_OP_DIV: return launch_typed<MX_COMPLEX64, MX_OP_DIV>(cdims, shape, sR, sA, sB, R, A, B, total, st);
+        default:
+            return fail(MX_ERR_UNSUPPORTED, "mx_launch_bcast_binary: Complex64 has Add / Sub / Mul / Divide only (op " +
+                                                std::to_string(op) + ")");
+        }
+    }
     int rc = MX_OK;
     bool ok = dispatch_dtype(dtype, [&](auto dt) {
         rc = launch_op<decltype(dt)::value>(op, cdims, shape, sR, sA, sB, R, A, B, total, st);

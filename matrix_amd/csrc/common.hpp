@@ -104,6 +104,17 @@ template <> struct dt_traits<MX_BFLOAT16> {
     __device__ __forceinline__ static S st(C x) { return float_to_bf16(x); }
 };
 
+// complex64 (type code 9, complex.h:18-26): two floats, re first, 8-byte aligned (numpy's
+// complex64, float2).
+struct alignas(8) c64 { float re, im; };
+template <> struct dt_traits<MX_COMPLEX64> {
+    using S = c64; using C = c64;
+    static constexpr bool is_float = false;
+    static constexpr bool is_signed = true;
+    __device__ __forceinline__ static C ld(S x) { return x; }
+    __device__ __forceinline__ static S st(C x) { return x; }
+};
+
 inline size_t dtype_size(int dt) {
     switch (dt) {
     case MX_FLOAT32: case MX_INT32: case MX_UINT32: return 4;

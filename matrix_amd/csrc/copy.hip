@@ -10,7 +10,12 @@
 //     saturate to the 32-bit range first and then keep the low bits, as arm64's fcvtzs /
 //     fcvtzu followed by a narrowing store do;
 //   - integer -> integer keeps the low bits (two's complement);
-//   - anything -> bool is (value != 0); bool reads as 0 / 1.
+//   - anything -> bool is (value != 0); bool reads as 0 / 1;
+//   - a real dtype -> complex64 is complex64(float(value), 0), the complex64(float re, float im = 0)
+//     constructor static_cast picks (complex.h:22); complex64 defines no conversion to a real type,
+//     so complex64 -> real is rejected;
+//   - a copy within one dtype moves the element's bits (the blit and CopyInplaceGPU_<t>_<t> of the
+//     reference, static_cast<T>(T)), complex64 included.
 //
 // Layout: the iteration space is a collapsed descriptor (any cdims <= 8).  Same-dtype copies
 // whose innermost axis is unit-stride on both sides move 16 bytes per thread; same-dtype
@@ -75,7 +80,9 @@ template <int DD>
 __device__ __forceinline__ typename dt_traits<DD>::S narrow(const Wide& w) {
     using Tr = dt_traits<DD>;
     using S = typename Tr::S;
-    if constexpr (Tr::is_float) {
+    if constexpr (DD == MX_COMPLEX64) {
+        return c64{w.kind == 0 ? w.f : (w.kind == 1 ? (float)w.i : (float)w.u), 0.0f};
+    } else if constexpr (Tr::is_float) {
         const float v = w.kind == 0 ? w.f : (w.kind == 1 ? (float)w.i : (float)w.u);
         return Tr::st(v);
     } else if constexpr (DD == MX_BOOL) {
@@ -255,10 +262,12 @@ extern "C" int mx_launch_copy_strided(int dst_dtype, int src_dtype, int cdims, c
     if (cdims < 0 || cdims > MX_MAX_DIMS)
         return fail(MX_ERR_INVALID_ARG, "mx_launch_copy_strided: cdims " + std::to_string(cdims) + " outside [0, 8]");
     if (cdims > 0 && (!shape || !sDst || !sSrc)) return fail(MX_ERR_INVALID_ARG, "mx_launch_copy_strided: null descriptor");
-    if (dtype_size(dst_dtype) == 0 || dtype_size(src_dtype) == 0 || dst_dtype == MX_COMPLEX64 ||
-        src_dtype == MX_COMPLEX64)
+    if (dtype_size(dst_dtype) == 0 || dtype_size(src_dtype) == 0)
         return fail(MX_ERR_UNSUPPORTED, "mx_launch_copy_strided: no kernel for dtypes " + std::to_string(dst_dtype) +
                                             " <- " + std::to_string(src_dtype));
+    if (src_dtype == MX_COMPLEX64 && dst_dtype != MX_COMPLEX64)
+        return fail(MX_ERR_UNSUPPORTED, "mx_launch_copy_strided: Complex64 has no cast to a real dtype (" +
+                                            std::to_string(dst_dtype) + ")");
     uint64_t total = 1;
     for (int k = 0; k < cdims; k++) total *= shape[k];
     if (total == 0) return MX_OK;
@@ -311,11 +320,26 @@ extern "C" int mx_launch_copy_strided(int dst_dtype, int src_dtype, int cdims, c
     const uint64_t want = (total + 255) / 256;
     const uint32_t blocks = (uint32_t)(want < 65536 ? want : 65536);
     int rc = MX_OK;
-    dispatch_pair(dst_dtype, src_dtype, [&](auto D, auto S) {
+    auto launch = [&](auto D, auto S) {
         constexpr int DD = decltype(D)::value, SD = decltype(S)::value;
         hipLaunchKernelGGL((copy_scalar_kernel<DD, SD>), dim3(blocks), dim3(256), 0, st,
                            (typename dt_traits<DD>::S*)dst, (const typename dt_traits<SD>::S*)src, total, d);
         if (hipGetLastError() != hipSuccess) rc = fail(MX_ERR_HIP, "mx_launch_copy_strided: launch failed");
-    });
+    };
+    if (dst_dtype == src_dtype) {                  // bits, through the unsigned carrier of the element size
+        switch (es) {
+        case 1: launch(std::integral_constant<int, MX_UINT8>{}, std::integral_constant<int, MX_UINT8>{}); break;
+        case 2: launch(std::integral_constant<int, MX_UINT16>{}, std::integral_constant<int, MX_UINT16>{}); break;
+        case 4: launch(std::integral_constant<int, MX_UINT32>{}, std::integral_constant<int, MX_UINT32>{}); break;
+        default: launch(std::integral_constant<int, MX_UINT64>{}, std::integral_constant<int, MX_UINT64>{}); break;
+        }
+        return rc;
+    }
+    if (dst_dtype == MX_COMPLEX64) {
+        if (!dispatch_dtype(src_dtype, [&](auto S) { launch(std::integral_constant<int, MX_COMPLEX64>{}, S); }))
+            return fail(MX_ERR_UNSUPPORTED, "mx_launch_copy_strided: no kernel for dtype " + std::to_string(src_dtype));
+        return rc;
+    }
+    dispatch_pair(dst_dtype, src_dtype, launch);
     return rc;
 }

@@ -5,6 +5,16 @@
 // 16-bit floats compute in float and round once; integers wrap; integer division truncates, a
 // zero divisor gives 0 and MIN / -1 gives MIN (arm64); Max is (a < b) ? b : a and Min is
 // (b < a) ? b : a on the operands' own bits; Equal writes 1 / 0 in the operands' dtype.
+// complex64 has Add / Sub / Mul / Divide only (the reference instantiates its broadcast
+// kernels for type 9 in those four, BrodcastedMul.metal:95), with complex.h's arithmetic:
+//   (a + bi) +- (c + di) = (a +- c) + (b +- d)i;
+//   (a + bi)(c + di) = (a, b) c + (-b, a) d (complex.h:36-38), which clang's default contraction
+//     (-ffp-contract=on) makes one rounded product and one fused multiply-add per part:
+//     re = fma(a, c, -(b d)), im = fma(b, c, a d);
+//   (a + bi) / (c + di) = ((a + bi)(c - di)) / (c c + d d) (complex.h:40-52): the product as
+//     above with conj(rhs) = (c, -d), then both parts divided (IEEE) by c c + d d, whose two
+//     squares are each rounded (simd_length_squared sums outside the expression).  No scaling:
+//     |rhs| beyond ~1.8e19 overflows c c + d d, as in the reference.
 #pragma once
 #include "common.hpp"
 
@@ -15,7 +25,22 @@ struct BinOp {
     using Tr = dt_traits<DT>;
     using S = typename Tr::S;
     __device__ __forceinline__ static S apply(S a, S b) {
-        if constexpr (Tr::is_float) {
+        if constexpr (DT == MX_COMPLEX64) {
+#pragma clang fp contract(off)
+            static_assert(OP == MX_OP_ADD || OP == MX_OP_SUB || OP == MX_OP_MUL || OP == MX_OP_DIV,
+                          "complex64: Add / Sub / Mul / Divide only");
+            if constexpr (OP == MX_OP_ADD) return c64{a.re + b.re, a.im + b.im};
+            else if constexpr (OP == MX_OP_SUB) return c64{a.re - b.re, a.im - b.im};
+            else if constexpr (OP == MX_OP_MUL) return c64{__builtin_fmaf(a.re, b.re, -(a.im * b.im)),
+                                                           __builtin_fmaf(a.im, b.re, a.re * b.im)};
+            else {
+                const float c = b.re, d = -b.im;                 // conj(rhs)
+                const float re = __builtin_fmaf(a.re, c, -(a.im * d));
+                const float im = __builtin_fmaf(a.im, c, a.re * d);
+                const float m = b.re * b.re + b.im * b.im;
+                return c64{re / m, im / m};
+            }
+        } else if constexpr (Tr::is_float) {
             float x = Tr::ld(a), y = Tr::ld(b);
             if constexpr (OP == MX_OP_ADD) return Tr::st(x + y);
             else if constexpr (OP == MX_OP_SUB) return Tr::st(x - y);

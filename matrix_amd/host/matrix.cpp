@@ -78,6 +78,7 @@ void store_value(dtype type, double v, uint8_t* dst) {
     case dtype::UInt32: { uint32_t x = (uint32_t)(int64_t)v; std::memcpy(dst, &x, 4); break; }
     case dtype::Int64: { int64_t x = (int64_t)v; std::memcpy(dst, &x, 8); break; }
     case dtype::UInt64: { uint64_t x = (uint64_t)v; std::memcpy(dst, &x, 8); break; }
+    case dtype::Complex64: { const float c[2] = {(float)v, 0.0f}; std::memcpy(dst, c, 8); break; }
     default: throw std::invalid_argument("matrix: unsupported dtype");
     }
 }
@@ -762,9 +763,17 @@ struct ConvPrim : Primitive {
 };
 
 // The operands are cast to their promoted dtype first, as operator+ does (Matrix.mm:8312-8315).
+// Ops the reference runs on real dtypes only (dispatch_type throws for Complex64, matrix.h:327-330,
+// and no GPU kernel of theirs is instantiated for type 9).
+void require_real(dtype t, const char* who) {
+    if (is_complex(t)) throw std::runtime_error(std::string("matrix::") + who + ": Complex64 is not supported by this op");
+}
+
 matrix binary(int op, const matrix& x, const matrix& y) {
     if (!x.storage || !y.storage) throw std::invalid_argument("matrix: operand is empty");
     const dtype t = promote_types(x.type, y.type);
+    if (op == MX_OP_MAX || op == MX_OP_MIN || op == MX_OP_EQ)
+        require_real(t, op == MX_OP_MAX ? "max" : op == MX_OP_MIN ? "min" : "equal");
     matrix a = x.type == t ? x : x.astype(t);
     matrix b = y.type == t ? y : y.astype(t);
     uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
@@ -778,6 +787,7 @@ matrix binary(int op, const matrix& x, const matrix& y) {
 
 matrix reduce(int op, const matrix& x, int axis, bool keepdims, const char* who) {
     if (x.dims == 0) throw std::invalid_argument(std::string("matrix::") + who + ": rank-0 input");
+    require_real(x.type, who);
     axis = norm_axis(axis, x.dims, who);
     std::vector<size_m> shape;
     for (uint32_t i = 0; i < x.dims; i++) {
@@ -848,8 +858,10 @@ matrix matrix::broadcast_to(const std::vector<size_m>& shape) const {
                      std::make_shared<ViewPrim>(ViewPrim::Broadcast, *this, std::vector<size_m>{}, shape));
 }
 
+// A real dtype casts to Complex64 as (float(v), 0) (complex.h:22); Complex64 has no cast to a real dtype.
 matrix matrix::astype(dtype t, bool make_contig) const {
     if (t == type && (!make_contig || is_contiguous())) return *this;
+    if (is_complex(type) && !is_complex(t)) throw std::runtime_error("matrix::astype: Complex64 has no cast to a real dtype");
     return make_node(shp_, t, std::make_shared<CopyPrim>(*this, t));
 }
 
@@ -909,6 +921,8 @@ static bool n_major_ok(const matrix& a, const matrix& bt) {
 // reference does (Matrix.mm:7068-7092) -- except a float B that is already N-major.
 matrix matrix::dot(const matrix& b, bool transposeB) const {
     if (dims < 2 || b.dims < 2) throw std::invalid_argument("matrix::dot requires both matrices to be at least 2D");
+    require_real(type, "dot");
+    require_real(b.type, "dot");
     matrix bt = b;
     if (!transposeB) {
         std::vector<size_m> axes(b.dims);
@@ -941,6 +955,7 @@ matrix matrix::conv(const matrix& input, const matrix& kernel, const std::vector
     chk(stride, "stride"); chk(pad_lo, "padding"); chk(pad_hi, "padding"); chk(kernel_dilation, "kernel dilation");
     chk(input_dilation, "input dilation");
     if (input.type != kernel.type) throw std::invalid_argument("matrix::conv: input and kernel dtypes differ");
+    require_real(input.type, "conv");
     if (groups < 1 || input.shape()[ns + 1] % groups || kernel.shape()[0] % groups ||
         input.shape()[ns + 1] / groups != kernel.shape()[ns + 1])
         throw std::invalid_argument("matrix::conv: channels do not match the kernel and groups");

@@ -15,6 +15,7 @@
 //     thread's stream with a single wait at the end.
 #pragma once
 
+#include <complex>
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
@@ -67,6 +68,7 @@ template <typename T> constexpr dtype dtype_of() {
     else if constexpr (std::is_same_v<T, int>) return dtype::Int32;
     else if constexpr (std::is_same_v<T, _Float16>) return dtype::Float16;
     else if constexpr (std::is_same_v<T, __bf16>) return dtype::BFloat16;
+    else if constexpr (std::is_same_v<T, std::complex<float>>) return dtype::Complex64;
     else static_assert(sizeof(T) == 0, "no dtype for this C++ type");
 }
 

@@ -185,10 +185,41 @@ static inline uint64_t idiv_u(uint64_t a, uint64_t b) { return b == 0 ? 0 : a / 
     default: return -1;                                                                      \
     }
 
+/* complex64, complex.h:18-52: {re, im} floats.  Multiply is (a, b)c + (-b, a)d
+ * (complex.h:36-38); clang's default -ffp-contract=on fuses the first product into the add:
+ * re = fma(a, c, -(b d)), im = fma(b, c, a d).  Divide multiplies by conj(rhs) = (c, -d) the same
+ * way and divides both parts by mag_sq(rhs) = c c + d d, whose squares are rounded separately
+ * (complex.h:40-52).  The reference has complex64 kernels for these four ops only
+ * (BrodcastedAdd.metal:95 and siblings). */
+typedef struct { float re, im; } orc_c64;
+static inline orc_c64 c64_add(orc_c64 x, orc_c64 y) { orc_c64 r = {x.re + y.re, x.im + y.im}; return r; }
+static inline orc_c64 c64_sub(orc_c64 x, orc_c64 y) { orc_c64 r = {x.re - y.re, x.im - y.im}; return r; }
+static inline orc_c64 c64_mul(orc_c64 x, orc_c64 y) {
+    orc_c64 r = {fmaf(x.re, y.re, -(x.im * y.im)), fmaf(x.im, y.re, x.re * y.im)};
+    return r;
+}
+static inline orc_c64 c64_div(orc_c64 x, orc_c64 y) {
+    orc_c64 cj = {y.re, -y.im};
+    orc_c64 p = c64_mul(x, cj);
+    float m = y.re * y.re + y.im * y.im;
+    orc_c64 r = {p.re / m, p.im / m};
+    return r;
+}
+
+#define BCAST_COMPLEX()                                                               \
+    switch (op) {                                                                     \
+    case ORC_ADD: BCAST_LOOP(orc_c64, orc_c64, c64_add(a, b)); return 0;              \
+    case ORC_SUB: BCAST_LOOP(orc_c64, orc_c64, c64_sub(a, b)); return 0;              \
+    case ORC_MUL: BCAST_LOOP(orc_c64, orc_c64, c64_mul(a, b)); return 0;              \
+    case ORC_DIV: BCAST_LOOP(orc_c64, orc_c64, c64_div(a, b)); return 0;              \
+    default: return -1;                                                               \
+    }
+
 int orc_bcast_binary(int op, int dtype, int cdims, const uint32_t* shape,
                      const uint32_t* sR, const uint32_t* sA, const uint32_t* sB,
                      uint64_t total, void* R, const void* A, const void* B) {
     switch (dtype) {
+    case ORC_C64: BCAST_COMPLEX()
     case ORC_F32: BCAST_FLOATLIKE(float, LD_F32, ST_F32)
     case ORC_F16: BCAST_FLOATLIKE(uint16_t, LD_F16, ST_F16)
     case ORC_BF16: BCAST_FLOATLIKE(uint16_t, LD_BF16, ST_BF16)
@@ -578,11 +609,39 @@ static void wr(int dt, void* p, uint64_t off, elem_t e) {
     }
 }
 
+static size_t orc_size(int dt) {
+    switch (dt) {
+    case ORC_F32: case ORC_I32: case ORC_U32: return 4;
+    case ORC_F16: case ORC_BF16: case ORC_I16: case ORC_U16: return 2;
+    case ORC_U8: case ORC_I8: case ORC_BOOL: return 1;
+    case ORC_I64: case ORC_U64: case ORC_C64: return 8;
+    default: return 0;
+    }
+}
+
+/* One element of the copy.  Within one dtype the element's bytes move unchanged
+ * (static_cast<T>(T), and the reference's blit for contiguous copies, Matrix.mm:1719-1747);
+ * a real dtype -> complex64 is complex64(float(v), 0) (complex.h:22), float(v) as for a Float
+ * destination; complex64 -> a real dtype has no conversion in the reference's type. */
+static void copy_elem(int dst_dtype, int src_dtype, void* dst, uint64_t od, const void* src, uint64_t os) {
+    if (dst_dtype == src_dtype) {
+        size_t es = orc_size(dst_dtype);
+        memcpy((char*)dst + od * es, (const char*)src + os * es, es);
+    } else if (dst_dtype == ORC_C64) {
+        elem_t e = rd(src_dtype, src, os);
+        orc_c64 z = {e.kind == 0 ? e.f : (e.kind == 1 ? (float)e.i : (float)e.u), 0.0f};
+        ((orc_c64*)dst)[od] = z;
+    } else {
+        wr(dst_dtype, dst, od, rd(src_dtype, src, os));
+    }
+}
+
 int orc_copy_strided(int dst_dtype, int src_dtype, int cdims, const uint32_t* shape,
                      const uint32_t* sDst, const uint32_t* sSrc, uint64_t total,
                      void* dst, const void* src) {
-    if (dst_dtype == ORC_C64 || src_dtype == ORC_C64 || dst_dtype > 12 || src_dtype > 12) return -1;
-    if (cdims == 0) { wr(dst_dtype, dst, 0, rd(src_dtype, src, 0)); return 0; }
+    if (dst_dtype < 0 || src_dtype < 0 || dst_dtype > 12 || src_dtype > 12) return -1;
+    if (src_dtype == ORC_C64 && dst_dtype != ORC_C64) return -1;
+    if (cdims == 0) { copy_elem(dst_dtype, src_dtype, dst, 0, src, 0); return 0; }
     for (uint64_t gid = 0; gid < total; gid++) {
         uint64_t rem = gid, od = 0, os = 0;
         for (int d = cdims - 1; d >= 0; --d) {
@@ -590,7 +649,7 @@ int orc_copy_strided(int dst_dtype, int src_dtype, int cdims, const uint32_t* sh
             od += idx * sDst[d]; os += idx * sSrc[d];
             rem /= shape[d];
         }
-        wr(dst_dtype, dst, od, rd(src_dtype, src, os));
+        copy_elem(dst_dtype, src_dtype, dst, od, src, os);
     }
     return 0;
 }

@@ -15,6 +15,7 @@
  *   orc_batched_matmul Matrix.mm:7108-7196 (dot_cpu / batched_dot_cpu)
  *   orc_conv           Matrix.mm:12397-12500 (conv_cpu) == Matrix.mm:5668-5741 (conv2d_cpu)
  *   orc_copy_strided   matrix.h:1337-1550 (copyCPUinplace / copyCPUinplaceTypeCasted)
+ *   complex64          complex.h:18-52 (Add / Sub / Mul / Divide; real -> complex64 casts)
  *
  * Element codes are the reference's dtype codes (matrix.h:35-52).
  * Strides and shapes are element counts in uint32 (Utils.h:125 size_m).

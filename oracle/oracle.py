@@ -23,6 +23,7 @@ ACC_LITERAL, ACC_F32 = 0, 1
 NP_DTYPE = {
     F32: np.float32, F16: np.float16, U8: np.uint8, I32: np.int32, I16: np.int16, U32: np.uint32,
     U16: np.uint16, BOOL: np.bool_, I8: np.int8, BF16: np.uint16, I64: np.int64, U64: np.uint64,
+    C64: np.complex64,
 }
 
 _lib = None

@@ -10,6 +10,7 @@
 #include "../../include/matrix_amd.h"
 
 #include <cmath>
+#include <complex>
 #include <cstdio>
 #include <cstring>
 #include <unordered_set>
@@ -633,6 +634,73 @@ CASE(gpu_value_and_grad) {
     }
 }
 
+// complex64 (type code 9): Add / Sub / Mul / Divide build and promote real operands (a real leaf
+// next to a complex one is cast to complex64); the ops the reference has no complex64 path for
+// (max / min / equal, the reductions, dot, conv, a cast back to a real dtype) throw at construction.
+template <typename F>
+static bool throws_runtime(F&& f) {
+    try { f(); } catch (const std::runtime_error&) { return true; }
+    return false;
+}
+
+CASE(complex_construction_rules) {
+    using cf = std::complex<float>;
+    matrix z = matrix::from_host<cf>({4, 3}, std::vector<cf>(12, cf(1.0f, 2.0f)));
+    matrix r = matrix::from_host<float>({3}, std::vector<float>(3, 0.5f));
+    EXPECT(z.type == dtype::Complex64, "std::complex<float> leaf is not Complex64");
+    matrix p = z * r;
+    EXPECT(p.type == dtype::Complex64 && p.shape_vec() == std::vector<size_m>({4, 3}), "complex * real: dtype / shape");
+    EXPECT((r + z).type == dtype::Complex64 && (z / z).type == dtype::Complex64 && (z - r).type == dtype::Complex64,
+           "complex arithmetic dtype");
+    EXPECT(r.astype(dtype::Complex64).type == dtype::Complex64, "real -> complex64 cast");
+    EXPECT(throws_runtime([&] { matrix::max(z, z); }), "max of complex64 did not throw");
+    EXPECT(throws_runtime([&] { matrix::min(z, r); }), "min of complex64 did not throw");
+    EXPECT(throws_runtime([&] { matrix::equal(z, z); }), "equal of complex64 did not throw");
+    EXPECT(throws_runtime([&] { z.sum(1); }), "sum of complex64 did not throw");
+    EXPECT(throws_runtime([&] { z.argmax(0); }), "argmax of complex64 did not throw");
+    EXPECT(throws_runtime([&] { z.dot(z.transpose({1, 0})); }), "dot of complex64 did not throw");
+    EXPECT(throws_runtime([&] { z.astype(dtype::Float); }), "complex64 -> Float did not throw");
+}
+
+// (a * b - c) / (a + b) with a [64, 33] complex64, b [33] complex64 broadcast over rows and c a
+// float32 [64, 1] column promoted to complex64, against complex128 host arithmetic on the same
+// float32 inputs: each part within 16 u of the operands' magnitudes (mul, sub, add and div each
+// round a few times); a swapped part or wrong sign is O(1) off.  Plus a transposed complex view
+// made contiguous (a bit-exact move).
+CASE(gpu_complex64_arithmetic) {
+    using cf = std::complex<float>;
+    using cd = std::complex<double>;
+    const size_m R = 64, Cc = 33;
+    auto ar = randn((size_t)R * Cc * 2, 70), br = randn((size_t)Cc * 2, 71), cv = randn(R, 72);
+    std::vector<cf> av(R * Cc), bv(Cc);
+    for (size_t i = 0; i < av.size(); i++) av[i] = cf(ar[2 * i], ar[2 * i + 1]);
+    for (size_t i = 0; i < bv.size(); i++) bv[i] = cf(br[2 * i], br[2 * i + 1]);
+    matrix a = matrix::from_host<cf>({R, Cc}, av);
+    matrix b = matrix::from_host<cf>({Cc}, bv);
+    matrix c = matrix::from_host<float>({R, 1}, cv);
+    matrix y = (a * b - c) / (a + b);
+    matrix t = a.transpose({1, 0}).astype(dtype::Complex64, true);
+    std::vector<matrix> outs{y, t};
+    matrix::eval(outs);
+    EXPECT(y.type == dtype::Complex64, "result dtype");
+    auto yg = y.to_host<cf>();
+    auto tg = t.to_host<cf>();
+    const double u = std::ldexp(1.0, -24);
+    for (size_t r = 0; r < R; r++)
+        for (size_t j = 0; j < Cc; j++) {
+            const cd A(av[r * Cc + j]), B(bv[j]), C(cv[r], 0.0);
+            const cd num = A * B - C, den = A + B;
+            const cd want = num / den;
+            const double scale = (std::abs(A) * std::abs(B) + std::abs(C) + 4 * std::abs(den) * std::abs(want)) /
+                                 std::abs(den);
+            const cd got(yg[r * Cc + j]);
+            EXPECT(std::abs(got.real() - want.real()) <= 16 * u * scale &&
+                       std::abs(got.imag() - want.imag()) <= 16 * u * scale,
+                   "complex (a*b - c)/(a + b) at " + std::to_string(r) + "," + std::to_string(j));
+            EXPECT(std::memcmp(&tg[j * R + r], &av[r * Cc + j], sizeof(cf)) == 0, "complex transpose copy");
+        }
+}
+
 int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "cpu";
     if (mode == "cpu") {
@@ -640,6 +708,7 @@ int main(int argc, char** argv) {
         run("shapes_dot_and_conv", shapes_dot_and_conv);
         run("views_share_storage", views_share_storage);
         run("grad_graph_structure", grad_graph_structure);
+        run("complex_construction_rules", complex_construction_rules);
     } else {
         run("gpu_add_then_rowsum", gpu_add_then_rowsum);
         run("gpu_fused_reduction_lifecycle", gpu_fused_reduction_lifecycle);
@@ -650,6 +719,7 @@ int main(int argc, char** argv) {
         run("gpu_conv2d_nchw_views", gpu_conv2d_nchw_views);
         run("gpu_mlp_training_step_compile_once", gpu_mlp_training_step_compile_once);
         run("gpu_value_and_grad", gpu_value_and_grad);
+        run("gpu_complex64_arithmetic", gpu_complex64_arithmetic);
     }
     return g_fail ? 1 : 0;
 }

@@ -59,8 +59,8 @@ def test_invalid_arguments_fail_without_gpu():
 def test_unsupported_dtype_and_uninitialized_runtime():
     shape = mx.u32([4])
     st = mx.u32([1])
-    # complex64 has no kernel in this build
-    rc = mx.lib.mx_launch_bcast_binary(0, mx.COMPLEX64, 1, shape, st, st, st, 8, 8, 8, ctypes.c_void_p(1))
+    # complex64 has no Max kernel (the reference instantiates Add / Sub / Mul / Divide only)
+    rc = mx.lib.mx_launch_bcast_binary(mx.OP_MAX, mx.COMPLEX64, 1, shape, st, st, st, 8, 8, 8, ctypes.c_void_p(1))
     assert rc in (mx.ERR_UNSUPPORTED, mx.ERR_NOT_INITIALIZED)
     p = ctypes.c_void_p()
     if not mx._initialized:

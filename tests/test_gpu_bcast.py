@@ -154,3 +154,41 @@ def test_strided_view_operand(mx, orc):
     got, ref = run_pair(mx, orc, mx.OP_ADD, mx.FLOAT32, base, b, a_shape=[40, 48], a_strides=[1, 40])
     assert np.array_equal(bits(got), bits(ref))
     assert np.array_equal(got.reshape(40, 48), base.T + b)
+
+
+def complex_data(rng, shape):
+    z = rng.standard_normal(list(shape) + [2]).astype(np.float32) * 4
+    z[rng.random(shape) < 0.05] = 0.0                                   # zeros in both parts
+    return z.view(np.complex64).reshape(shape)
+
+
+def assert_complex_match(got, ref):
+    """Bit-exact per part; a NaN part matches any NaN (0 / 0 from a zero divisor)."""
+    g, r = got.view(np.float32), ref.view(np.float32)
+    bad = (bits(g) != bits(r)) & ~(np.isnan(g) & np.isnan(r))
+    assert not bad.any(), f"{int(bad.sum())} mismatching float parts, first at {int(np.argmax(bad))}"
+
+
+@pytest.mark.parametrize("opn", ["OP_ADD", "OP_SUB", "OP_MUL", "OP_DIV"])
+def test_complex64_ops(mx, orc, opn):
+    """complex64 Add / Sub / Mul / Divide (complex.h:28-52) on the 16-byte path (even inner
+    extent), the gather path (odd inner extent, row broadcast), rank-0 and a misaligned view."""
+    op = getattr(mx, opn)
+    rng = np.random.default_rng(300 + op)
+    for sa, sb in [([64, 96], [1, 96]), ([5, 7, 3], [7, 1]), ([33], [33]), ([8, 1], [1, 40]), ([256, 1024], [1024])]:
+        a, b = complex_data(rng, sa), complex_data(rng, sb)
+        got, ref = run_pair(mx, orc, op, mx.COMPLEX64, a, b)
+        assert_complex_match(got, ref)
+    a, b = complex_data(rng, []), complex_data(rng, [])
+    got, ref = run_pair(mx, orc, op, mx.COMPLEX64, a, b, a_shape=[], b_shape=[])
+    assert_complex_match(got, ref)
+    a, b = complex_data(rng, [48, 32]), complex_data(rng, [48, 32])
+    got, ref = run_pair(mx, orc, op, mx.COMPLEX64, a, b, offset_elems=1)
+    assert_complex_match(got, ref)
+
+
+def test_complex64_has_no_ordering_ops(mx):
+    A = mx.DeviceBuffer(64)
+    for op in (mx.OP_MAX, mx.OP_MIN, mx.OP_EQ):
+        with pytest.raises(mx.MatrixAMDError):
+            mx.launch_bcast_binary(op, mx.COMPLEX64, ([4], [1], [1], [1]), A.ptr, A.ptr, A.ptr)

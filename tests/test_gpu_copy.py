@@ -139,3 +139,50 @@ def test_transposes(mx, orc, shape, perm, dt):
     mx.sync()
     got = Y.download(x.dtype, x.size)
     assert np.array_equal(bits(got), bits(x.reshape(shape).transpose(perm).ravel()))
+
+
+@pytest.mark.parametrize("shape,perm", [
+    ([64, 48], (1, 0)),                  # 16-byte register-block transpose
+    ([3, 128, 40], (0, 1, 2)),           # contiguous rows: 16-byte path
+    ([2, 3, 4, 5, 6], (4, 0, 3, 1, 2)),  # gather
+    ([10, 4097], (1, 0)),                # odd extent: gather
+])
+def test_complex64_views_move_bits(mx, orc, shape, perm):
+    """complex64 -> complex64 moves the 8 bytes of every element (NaN payloads and -0 kept)."""
+    rng = np.random.default_rng(5)
+    n = int(np.prod(shape))
+    x = rng.standard_normal(2 * n).astype(np.float32)
+    x[:6] = [np.nan, -0.0, np.inf, -np.inf, 1e-45, -3.0]
+    x = x.view(np.complex64)
+    st = contiguous_strides(shape)
+    vshape = [shape[p] for p in perm]
+    desc = mx.collapse_dims2(vshape, contiguous_strides(vshape), [st[p] for p in perm])
+    X = mx.DeviceBuffer.from_numpy(x)
+    Y = mx.DeviceBuffer(x.nbytes)
+    mx.launch_copy_strided(mx.COMPLEX64, mx.COMPLEX64, desc, Y.ptr, X.ptr)
+    mx.sync()
+    got = Y.download(np.complex64, n)
+    assert np.array_equal(bits(got), bits(x.reshape(shape).transpose(perm).ravel()))
+
+
+@pytest.mark.parametrize("src", list(NP))
+def test_real_to_complex64(mx, orc, src):
+    """A real dtype -> complex64 is (float(v), 0), strided source, against the oracle."""
+    rng = np.random.default_rng(len(src) + 90)
+    x = values(src, 2000, rng)
+    desc = ([40, 25], [25, 1], [1, 40])              # a transposed source view
+    X = mx.DeviceBuffer.from_numpy(x)
+    Y = mx.DeviceBuffer(1000 * 8)
+    mx.launch_copy_strided(mx.COMPLEX64, getattr(mx, src), desc, Y.ptr, X.ptr)
+    mx.sync()
+    got = Y.download(np.complex64, 1000)
+    ref = orc.copy_strided(orc.C64, getattr(orc, orc_code(src)), [40, 25], [25, 1], [1, 40],
+                           np.zeros(1000, np.complex64), x)
+    g, r = got.view(np.float32), ref.view(np.float32)
+    assert not ((bits(g) != bits(r)) & ~(np.isnan(g) & np.isnan(r))).any()
+
+
+def test_complex64_to_real_is_rejected(mx):
+    X = mx.DeviceBuffer(64)
+    with pytest.raises(mx.MatrixAMDError):
+        mx.launch_copy_strided(mx.FLOAT32, mx.COMPLEX64, ([4], [1], [1]), X.ptr, X.ptr)

@@ -20,4 +20,4 @@ def ensure_built():
 def test_graph_building_cpu():
     out = subprocess.run([str(ensure_built()), "cpu"], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stdout + out.stderr
-    assert "FAIL" not in out.stdout and out.stdout.count("PASS") == 4, out.stdout
+    assert "FAIL" not in out.stdout and out.stdout.count("PASS") == 5, out.stdout

@@ -395,3 +395,119 @@ def test_copy_transpose_and_cast(orc):
     dsti = np.zeros(120, np.int32)
     orc.copy_strided(orc.I32, orc.F32, shape, contiguous_strides(shape), s_src, dsti, src)
     assert np.array_equal(dsti, np.trunc(src.transpose(2, 0, 1)).astype(np.int32).ravel())
+
+
+# ------------------------------------------------------------------ complex64
+U32 = 2.0 ** -24      # unit roundoff of float32
+
+
+def _c64(rng, n, scale=4.0):
+    z = (rng.standard_normal(n) * scale + 1j * rng.standard_normal(n) * scale).astype(np.complex64)
+    return z
+
+
+def _bin(orc, op, a, b):
+    n = a.size
+    return orc.bcast_binary(op, orc.C64, ([n], [1], [1], [1]), n, a, b)
+
+
+def test_complex_add_sub_are_componentwise_float32(orc):
+    """Add / Sub are per-part float32 sums (complex.h:28-34): numpy's complex64 arithmetic."""
+    rng = np.random.default_rng(40)
+    a, b = _c64(rng, 4096), _c64(rng, 4096)
+    assert np.array_equal(bits(_bin(orc, orc.ADD, a, b)), bits(a + b))
+    assert np.array_equal(bits(_bin(orc, orc.SUB, a, b)), bits(a - b))
+
+
+def test_complex_mul_div_within_rounding_of_exact(orc):
+    """Mul / Div against complex128 arithmetic on the same float32 inputs: each part within the
+    rounding the formula allows (2u of |a||c| + |b||d| for the product, 6u of
+    (|a| + |b|)(|c| + |d|) / |rhs|^2 for the quotient).  A swapped part, a wrong sign or a dropped
+    term is off by O(1)."""
+    rng = np.random.default_rng(41)
+    a, b = _c64(rng, 8192), _c64(rng, 8192)
+    A, B = a.astype(np.complex128), b.astype(np.complex128)
+    got = _bin(orc, orc.MUL, a, b).astype(np.complex128)
+    ex = A * B
+    sr = np.abs(A.real * B.real) + np.abs(A.imag * B.imag)
+    si = np.abs(A.imag * B.real) + np.abs(A.real * B.imag)
+    assert np.all(np.abs(got.real - ex.real) <= 2 * U32 * sr)
+    assert np.all(np.abs(got.imag - ex.imag) <= 2 * U32 * si)
+    got = _bin(orc, orc.DIV, a, b).astype(np.complex128)
+    ex = A / B
+    bound = 6 * U32 * (np.abs(A.real) + np.abs(A.imag)) * (np.abs(B.real) + np.abs(B.imag)) / np.abs(B) ** 2
+    assert np.all(np.abs(got.real - ex.real) <= bound)
+    assert np.all(np.abs(got.imag - ex.imag) <= bound)
+
+
+def test_complex_exact_special_cases(orc):
+    """z * 1 = z, z * i = (-b, a), z / 1 = z, i * i = -1: exact in the formula."""
+    rng = np.random.default_rng(42)
+    z = _c64(rng, 1000)
+    z = z[(z.real != 0) & (z.imag != 0)]
+    one = np.ones(z.size, np.complex64)
+    i = np.full(z.size, 1j, np.complex64)
+    assert np.array_equal(bits(_bin(orc, orc.MUL, z, one)), bits(z))
+    assert np.array_equal(bits(_bin(orc, orc.DIV, z, one)), bits(z))
+    want = (-z.imag + 1j * z.real).astype(np.complex64)
+    assert np.array_equal(bits(_bin(orc, orc.MUL, z, i)), bits(want))
+    assert _bin(orc, orc.MUL, i[:1], i[:1])[0] == -1
+
+
+def test_complex_mul_fuses_the_first_product(orc):
+    """(a + bi)(c + di) = (a, b) c + (-b, a) d with the first product fused: im of z * conj(z) is
+    fma(b, a, -fl(a b)) = a b - fl(a b), the exact rounding error of a b (the other fusion
+    gives its negative, an unfused product gives 0)."""
+    rng = np.random.default_rng(43)
+    z = _c64(rng, 2000)
+    got = _bin(orc, orc.MUL, z, np.conj(z))
+    ab = z.real.astype(np.float64) * z.imag.astype(np.float64)     # exact: 24 + 24 bits
+    err = ab - (z.real * z.imag).astype(np.float64)
+    assert np.array_equal(got.imag.astype(np.float64), err.astype(np.float32).astype(np.float64))
+    assert np.any(err != 0)
+
+
+def test_complex_div_is_unscaled(orc):
+    """Division by c c + d d without scaling (complex.h:50-52): |rhs| past ~1.8e19 overflows the
+    denominator to inf and gives 0; |rhs| below ~1e-23 underflows it to 0 and gives inf.  A scaled
+    (Smith) division would return 1e-20 and 1e30."""
+    a = np.array([1 + 1j, 1 + 0j], np.complex64)
+    b = np.array([1e20 + 0j, 1e-30 + 0j], np.complex64)
+    got = _bin(orc, orc.DIV, a, b)
+    assert got[0] == 0
+    assert np.isinf(got[1].real)
+
+
+def test_complex_rejects_ordering_ops(orc):
+    a = np.ones(4, np.complex64)
+    for op in (orc.MAX, orc.MIN, orc.EQ):
+        with pytest.raises(ValueError):
+            _bin(orc, op, a, a)
+
+
+def test_copy_complex_moves_bits_and_casts_from_real(orc):
+    """complex64 -> complex64 moves the 8 bytes (a transposed view here); a real dtype -> complex64
+    is (float(v), 0), numpy's astype for the dtypes it converts exactly; complex64 -> real has no
+    cast."""
+    rng = np.random.default_rng(44)
+    z = _c64(rng, 120).reshape(4, 5, 6)
+    z[0, 0, 0] = complex(np.nan, -0.0)
+    dst = np.zeros(120, np.complex64)
+    orc.copy_strided(orc.C64, orc.C64, [6, 4, 5], contiguous_strides([6, 4, 5]), [1, 30, 6], dst, z)
+    assert np.array_equal(bits(dst), bits(z.transpose(2, 0, 1).ravel()))
+    for code, x in ((orc.F32, rng.standard_normal(64).astype(np.float32)),
+                    (orc.F16, rng.standard_normal(64).astype(np.float16)),
+                    (orc.I32, rng.integers(-2**31, 2**31 - 1, 64, dtype=np.int32)),
+                    (orc.U8, rng.integers(0, 255, 64, dtype=np.uint8)),
+                    (orc.BOOL, rng.integers(0, 2, 64).astype(np.bool_))):
+        out = np.zeros(64, np.complex64)
+        orc.copy_strided(orc.C64, code, [64], [1], [1], out, x)
+        assert np.array_equal(bits(out), bits(x.astype(np.complex64))), code
+    x = rng.integers(-2**63, 2**63 - 1, 64, dtype=np.int64)
+    out = np.zeros(64, np.complex64)
+    f = np.zeros(64, np.float32)
+    orc.copy_strided(orc.C64, orc.I64, [64], [1], [1], out, x)
+    orc.copy_strided(orc.F32, orc.I64, [64], [1], [1], f, x)
+    assert np.array_equal(bits(out.real.copy()), bits(f)) and not out.imag.any()
+    with pytest.raises(ValueError):
+        orc.copy_strided(orc.F32, orc.C64, [4], [1], [1], np.zeros(4, np.float32), np.zeros(4, np.complex64))
