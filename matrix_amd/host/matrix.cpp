@@ -1381,12 +1381,12 @@ void matrix::eval() { std::vector<matrix> v{*this}; eval(v); }
 std::vector<uint8_t> matrix::to_host_bytes() const {
     const size_t es = dtype_size(type);
     std::vector<uint8_t> full;
-    if (tape) {
+    if (storage->host_is_source) {                      // a leaf's host values, or a view of them
+        full = storage->host;
+    } else if (tape) {
         if (!tape->evaluated) { matrix self = *this; self.eval(); }
         full.resize(storage->bytes);
         if (storage->bytes) check(mx_hip_d2h(full.data(), storage->dev, storage->bytes, nullptr), "device-to-host copy");
-    } else if (storage->host_is_source) {
-        full = storage->host;
     } else {                                            // a leaf whose values are on the device
         full.resize(storage->bytes);
         if (storage->bytes) check(mx_hip_d2h(full.data(), storage->dev, storage->bytes, nullptr), "device-to-host copy");

@@ -189,6 +189,14 @@ public:
                          int pad_h = 0, int pad_w = 0, int dilation_h = 1, int dilation_w = 1, int groups = 1,
                          int input_dilation_h = 1, int input_dilation_w = 1, bool flip = false);
 
+    // ---- files
+    // One uncompressed .npy per matrix (arr_0.npy, arr_1.npy, ...) in a STORED ZIP, byte for byte as
+    // the reference writes it (Matrix.mm:3748-4085, matrix.h:1237); evaluates each matrix first.
+    static void save_as_npz(std::vector<matrix> input, std::string file_path);
+    // Reads an .npz of STORED entries (save_as_npz's, or np.savez's) into host leaves, in archive
+    // order; names (optional) receives each entry's name without ".npy".  No reference counterpart.
+    static std::vector<matrix> load_npz(const std::string& file_path, std::vector<std::string>* names = nullptr);
+
     // ---- evaluation
     void eval();
     void compile_gpu();
