@@ -364,9 +364,17 @@ thread_local uint64_t t_exec_gen = 0;
 struct DotEpilogue {
     matrix bias, s;
     std::weak_ptr<matrix_amd::Storage> z, h;
+    std::weak_ptr<Primitive> add, actp;   // the Add and Max / Min nodes the Dot's launch stands in for
     int act = MX_OP_MAX;
     uint64_t gen = 0;
 };
+
+// A node scheduled by the execute now running on this thread (fused launches write a consumer's
+// output only then: an evaluated consumer is a boundary other streams may be reading).
+bool pending_now(const std::weak_ptr<Primitive>& w) {
+    auto p = w.lock();
+    return p && !p->evaluated && p->run_gen == t_exec_gen;
+}
 
 // MATRIX_AMD_FUSE_EPILOGUE=0 compiles Dot / Add / Max as three launches.
 bool epilogue_fusion_on() {
@@ -435,6 +443,7 @@ struct BinaryPrim : Primitive {
     uint32_t cd = 0;
     uint32_t cs[MX_MAX_DIMS], sA[MX_MAX_DIMS], sB[MX_MAX_DIMS], sR[MX_MAX_DIMS];
     std::weak_ptr<matrix_amd::Storage> fused_out;   // the fused reduction's output
+    std::weak_ptr<Primitive> fused_node;            // the fused reduction
     int fused_red_op = -1;
     uint32_t fused_n = 0;
     uint64_t fused_runs = 0;
@@ -469,7 +478,7 @@ struct BinaryPrim : Primitive {
     }
     void execute(const matrix& out) override {
         if (epi_of && epi_of->gen == t_exec_gen) return;   // the Dot's launch wrote this output just now
-        if (auto red = fused_out.lock(); red && red->dev && fused_red_op >= 0) {
+        if (auto red = fused_out.lock(); red && red->dev && fused_red_op >= 0 && pending_now(fused_node)) {
             check(mx_launch_bcast_binary_reduce_rows(op, fused_red_op, (int)a.type, (int)cd, cs, sR, sA, sB, fused_n,
                                                      dptr(out), dptr(a), dptr(b), red->dev, stream),
                   std::string("launch ") + name() + " + reduction");
@@ -579,6 +588,7 @@ struct ReducePrim : Primitive {
             return;
         if (!in.is_contiguous() || in.offset != 0 || (uint64_t)n * dtype_size(in.type) > 16384) return;
         bp->fused_out = out.storage;
+        bp->fused_node = out.tape;
         bp->fused_red_op = op;
         bp->fused_n = n;
         producer = bp;
@@ -646,7 +656,8 @@ struct DotPrim : Primitive {
             auto z = epi->z.lock(), h = epi->h.lock();
             const auto& bs = epi->bias.storage;
             const auto& ss = epi->s.storage;
-            if (z && h && z->dev && h->dev && bs->dev && !bs->dev_stale && ss->dev && !ss->dev_stale) {
+            if (z && h && z->dev && h->dev && bs->dev && !bs->dev_stale && ss->dev && !ss->dev_stale &&
+                pending_now(epi->add) && pending_now(epi->actp)) {
                 check(mx_launch_batched_matmul_bias_act((int)a.type, (int)cd, cs, sA, sB, sC, K, dptr(out), dptr(a),
                                                         dptr(bt), dptr(epi->bias), z->dev, epi->act, dptr(epi->s),
                                                         h->dev, ws.p, ws.bytes, stream),
@@ -695,6 +706,8 @@ void BinaryPrim::try_fuse_epilogue(const matrix& out) {
     e->s = b;
     e->z = a.storage;
     e->h = out.storage;
+    e->add = a.tape;
+    e->actp = out.tape;
     e->act = op;
     dot->epi = e;
     add->epi_of = e;
@@ -1306,6 +1319,7 @@ void run_schedule(const Schedule& sc, Executor& ex) {
     for (const matrix& l : sc.leaves)
         if (l.storage->dev_stale) l.storage->upload();      // leaf written on the host
     const auto& nodes = sc.nodes;
+    for (const matrix& n : nodes) n.tape->run_gen = t_exec_gen;
     for (size_t oi = 0; oi < sc.order.size(); oi++) {
         const int i = sc.order[oi];
         Primitive* p = nodes[i].tape.get();

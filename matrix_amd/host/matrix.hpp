@@ -411,4 +411,5 @@ public:
     uint64_t version = 1;
     uint64_t last_visited_pass_id = 0;
     void* stream = nullptr;        // the stream execute() launches on (set by the executor)
+    uint64_t run_gen = 0;          // the executing thread's execute count when this node was scheduled
 };

@@ -241,6 +241,19 @@ CASE(gpu_fused_reduction_lifecycle) {
         for (size_t j = 0; j < Cc; j++) mag += std::fabs(av[r * Cc + j] * bv[j]);
         EXPECT(std::fabs(s2g[r] - sg[r]) <= 2e-4 * mag, "late reduction");
     }
+    // the producer alone while its fused reduction stays evaluated (a boundary of this execute):
+    // the product is recomputed by the plain broadcast launch and the reduction keeps its values
+    auto av3 = randn((size_t)R * Cc, 50);
+    std::memcpy(a.host_data(), av3.data(), av3.size() * sizeof(float));
+    a.mark_changed();
+    std::vector<matrix> only_c{c};
+    matrix::clear_trace_checks(only_c);
+    matrix::execute_gpu(only_c);
+    auto cg3 = c.to_host<float>();
+    for (size_t i = 0; i < (size_t)R * Cc; i++) EXPECT(cg3[i] == av3[i] * bv[i % Cc], "product recomputed alone");
+    auto sg3 = s.to_host<float>();
+    EXPECT(std::memcmp(sg3.data(), sg.data(), sg.size() * sizeof(float)) == 0,
+           "an evaluated fused reduction was rewritten by its producer");
 }
 
 // A dense layer's bias + ReLU, h = max(x . W + b, 0): the Dot launches the product, the bias Add
@@ -296,6 +309,26 @@ CASE(gpu_dense_bias_relu_lifecycle) {
     matrix::clear_trace_checks(only_h);
     matrix::execute_gpu(only_h);
     check(xv2, bv2, "executing h alone");
+    // the product alone while z and h stay evaluated: the Dot runs without its epilogue, z and h
+    // keep their values
+    const auto zg0 = z.to_host<float>(), hg0 = h.to_host<float>();
+    auto xv3 = randn((size_t)R * K, 45);
+    std::memcpy(x.host_data(), xv3.data(), xv3.size() * sizeof(float));
+    x.mark_changed();
+    std::vector<matrix> only_t{t};
+    matrix::clear_trace_checks(only_t);
+    matrix::execute_gpu(only_t);
+    EXPECT(z.to_host<float>() == zg0 && h.to_host<float>() == hg0, "an evaluated epilogue was rewritten by the Dot");
+    auto tg3 = t.to_host<float>();
+    for (size_t r = 0; r < R; r++)
+        for (size_t j = 0; j < N; j++) {
+            double ref = 0, mag = 0;
+            for (size_t k = 0; k < K; k++) {
+                ref += (double)xv3[r * K + k] * wv[k * N + j];
+                mag += std::fabs((double)xv3[r * K + k] * wv[k * N + j]);
+            }
+            EXPECT(std::fabs(tg3[r * N + j] - ref) <= 1e-5 * mag + 1e-6, "product recomputed alone");
+        }
 }
 
 // Independent reductions with one descriptor run as group launches (horizontal fusion): five over

@@ -121,7 +121,7 @@ def test_conv2d_mfma(mx, orc, dt, case):
     # (N, C, H, W, O, stride_h, stride_w, layout): 1 x 1 kernels, no padding, stride > 1 -- only
     # the sampled positions are packed, then a stride-1 product over them
     (3, 20, 13, 11, 24, 3, 3, "nchw"),     # odd extents, channels zero-padded to the K pair
-    (2, 64, 9, 9, 16, 2, 2, "nhwc"),       # channels-last input with padded channels (f16: 64 -> 64)
+    (2, 40, 9, 9, 16, 2, 2, "nhwc"),       # channels-last input with padded channels (40 -> 64 / 64 / 64)
     (2, 48, 10, 12, 40, 2, 1, "nchw"),     # stride 2 along H only
     (1, 16, 7, 16, 8, 1, 4, "nhwc"),       # stride 4 along W only
 ])
@@ -142,6 +142,12 @@ def test_conv2d_1x1_strided_sampled_pack(mx, orc, dt, case):
     got, ref = run_conv(mx, orc, code, x, in_shape, in_st, wt, k_shape, k_st, [0, 0], [sh, sw])
     err = normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx))
     assert err <= TOL[dt], (dt, case, err)
+    # the same product as a stride-1 convolution over the sampled positions taken as a strided
+    # view: the ordinary pack path and one GEMM of the same M, N and K -- equal bit for bit
+    view_shape = [n, (h - 1) // sh + 1, (w - 1) // sw + 1, c]
+    view_st = [in_st[0], in_st[1] * sh, in_st[2] * sw, in_st[3]]
+    got1, _ = run_conv(mx, orc, code, x, view_shape, view_st, wt, k_shape, k_st, [0, 0], [1, 1])
+    assert np.array_equal(bits(got), bits(got1)), (dt, case)
 
 
 @pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16"])

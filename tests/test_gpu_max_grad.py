@@ -4,7 +4,8 @@ The vjp of Max / Min (primitives.cpp:2604-2608) is four broadcast launches: m = 
 mask_b = equal(b, m), then g * (1 - mask_b) for a and g * mask_b for b.  The fused launch must give
 their result bit for bit: ties (a == b, including +0 / -0) send g to b, NaN operands follow the
 select, and g * 0 keeps g's sign (-0 for negative g).  Shapes cover the ReLU of a dense layer
-(b a scalar), a bias row, ragged broadcasts on the one-element path and rank 0.
+(b a scalar), a bias row, ragged broadcasts on the one-element path and rank 0.  The fused launch
+is also checked against the same four steps run in the oracle.
 """
 import numpy as np
 import pytest
@@ -40,7 +41,7 @@ def values(rng, shape, special):
     return x
 
 
-def run_case(mx, code, op, sa, sb, seed, special=True):
+def run_case(mx, code, op, sa, sb, seed, special=True, orc=None):
     rng = np.random.default_rng(seed)
     npt = mx.NP_DTYPE[code]
     a = stored(mx, code, values(rng, sa, special))
@@ -73,6 +74,15 @@ def run_case(mx, code, op, sa, sb, seed, special=True):
     for side, (F, R) in enumerate([(FA, RA), (FB, RB)]):
         got, ref = F.download(npt, total), R.download(npt, total)
         assert np.array_equal(bits(got), bits(ref)), (code, op, sa, sb, side)
+    if orc is not None:
+        # the same four steps in the oracle (the reference's CPU loops), against the fused launch
+        flat = lambda v: np.ascontiguousarray(v).reshape(-1)
+        m = orc.bcast_binary(op, code, d_ab, total, flat(a), flat(b))
+        mb = orc.bcast_binary(orc.EQ, code, d_b_full, total, flat(b), m)
+        ma = orc.bcast_binary(orc.SUB, code, d_one, total, flat(stored(mx, code, [1.0])), mb)
+        for side, (F, mask) in enumerate([(FA, ma), (FB, mb)]):
+            want = orc.bcast_binary(orc.MUL, code, d_full, total, flat(g), mask)
+            assert np.array_equal(bits(F.download(npt, total)), bits(want)), ("oracle", code, op, sa, sb, side)
     return FA.download(npt, total), FB.download(npt, total)
 
 
@@ -85,8 +95,8 @@ def run_case(mx, code, op, sa, sb, seed, special=True):
     ([1, 5, 3], [7, 1, 3]),         # both broadcast
     ([], []),                       # rank 0
 ])
-def test_max_grad_equals_four_launches(mx, dt, opn, sa, sb):
-    run_case(mx, getattr(mx, dt), getattr(mx, opn), sa, sb, seed=len(sa) * 10 + len(sb))
+def test_max_grad_equals_four_launches(mx, orc, dt, opn, sa, sb):
+    run_case(mx, getattr(mx, dt), getattr(mx, opn), sa, sb, seed=len(sa) * 10 + len(sb), orc=orc)
 
 
 def test_max_grad_routes_ties_to_b(mx):
