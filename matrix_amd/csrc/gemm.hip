@@ -177,10 +177,13 @@ int launch_bias_act(const GemmArgs& g, const void* C, const Epi& e, hipStream_t 
 // read back from there.  (Loading the fragments straight from global memory makes every load
 // instruction touch 64 bytes of 16 rows; that form streamed 3.66 TB/s on A[8, 4096] x
 // Bt[4096, 4096] in f32 against 4.13 here.)  LDS position of 16-byte chunk c of row r: r * 32 + (c ^ r), so
-// the 16 rows of one fragment read fall in distinct banks.  The chunk's A fragments are loaded
-// before the next chunk's Bt loads are issued, so waiting for them never waits for the prefetch.
-// Per wave: two accumulators alternating by step, summed at the end, then the waves' tiles are
-// summed in wave order through LDS (deterministic).
+// the 16 rows of one fragment read fall in distinct banks.  For 16-bit data a chunk's A fragments
+// (L2 hits) are loaded together with its Bt rows, one chunk ahead, into two register buffers (the
+// loop runs two chunks per turn), so no L2 round trip is waited for between chunks (A[8, 4096] x
+// Bt[4096, 4096] f16: 9.2 -> 8.4 us).  fp32 loads a chunk's A fragments after staging its Bt rows
+// and before the next chunk's Bt loads (A one chunk ahead measured 16.6 -> 17.4 us there).  Per
+// wave: two accumulators alternating by step, summed at the end, then the waves' tiles are summed
+// in wave order through LDS (deterministic).
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
@@ -190,9 +193,10 @@ template <> struct SkinnyFrag<MX_FLOAT16> { using V = tile::h8v; };
 template <> struct SkinnyFrag<MX_BFLOAT16> { using V = tile::b8v; };
 
 // Waves per block (measured on A[8|16, K] x Bt[4096|8192, K], K = 4096 | 8192, for 4, 8 and 16
-// waves and for 512- and 1024-byte chunks: 8 waves of 512-byte chunks were fastest or within 3%
-// everywhere; rotating the waves' K ranges from block to block changed nothing).
-constexpr int kSkinnyWaves = 8;
+// waves and 512- and 1024-byte chunks: 512-byte chunks; 8 waves for fp32, 4 for 16-bit data,
+// whose waves then stream four chunks each instead of two; rotating the waves' K ranges from
+// block to block changed nothing; two chunks of Bt ahead instead of one was slower).
+template <int DT> constexpr int kSkinnyWaves = DT == MX_FLOAT32 ? 8 : 4;
 
 template <int DT>
 __device__ __forceinline__ f4v skinny_mma(typename SkinnyFrag<DT>::V b, typename SkinnyFrag<DT>::V a, f4v acc) {
@@ -224,7 +228,7 @@ bool skinny_ok(const GemmArgs& g, const void* A, const void* Bt) {
 // kw: K elements per wave (a multiple of one step).  CVEC: C columns are unit-stride and every
 // 4-column group starts 4-element aligned, so a lane's 4 results go out in one store.
 template <int DT, bool CVEC>
-__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
+__global__ __launch_bounds__(64 * kSkinnyWaves<DT>) void gemm_skinny_kernel(
     typename MmaTraits<DT>::S* __restrict__ C, const typename MmaTraits<DT>::S* __restrict__ A,
     const typename MmaTraits<DT>::S* __restrict__ Bt, GemmArgs g, uint32_t kw) {
     using S = typename MmaTraits<DT>::S;
@@ -236,7 +240,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
     constexpr uint32_t CPR = CH * 4;              // 16-byte pieces per row of a chunk
     constexpr uint32_t RPI = 64 / CPR;            // rows per load instruction
     constexpr uint32_t NL = 16 / RPI;             // load instructions per chunk
-    constexpr int W = kSkinnyWaves;
+    constexpr int W = kSkinnyWaves<DT>;
     __shared__ V stage[W][16 * CPR];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
     const S* arow = A + offA + (uint64_t)min(i, g.M - 1) * g.lda;
     V* st = stage[wave];
     const V zero = {};
-    V R[NL], fa[CH];
+    V R[NL], fa[2][CH];
     f4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
     // Every load is unconditional: an element at or beyond kend is read from element kbeg of the
     // same row instead (in bounds) and replaced by zero where it is used, so no branch separates
@@ -273,43 +277,75 @@ __global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_skinny_kernel(
 #pragma unroll
         for (int j = 0; j < (int)NL; j++) R[j] = ld_stream(reinterpret_cast<const V*>(bbase + lrow[j] + ee));
     };
-    auto stage_and_load_a = [&](uint32_t kc) __attribute__((always_inline)) {
+    auto load_a = [&](uint32_t kc, V (&f)[CH]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < (int)CH; s++) {
+            const uint32_t k = kc + s * KS + grp * CE;
+            f[s] = *reinterpret_cast<const V*>(arow + (k < kend ? k : kbeg));
+        }
+    };
+    auto stage_b = [&]() __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < (int)NL; j++) {
             const uint32_t r = RPI * j + lr;
             st[r * CPR + (lq ^ r)] = R[j];
         }
-#pragma unroll
-        for (int s = 0; s < (int)CH; s++) {
-            const uint32_t k = kc + s * KS + grp * CE;
-            fa[s] = *reinterpret_cast<const V*>(arow + (k < kend ? k : kbeg));
-        }
     };
-    auto compute = [&](uint32_t kc) __attribute__((always_inline)) {
+    auto compute = [&](uint32_t kc, const V (&f)[CH]) __attribute__((always_inline)) {
 #pragma unroll
         for (int s = 0; s < (int)CH; s++) {
             const bool ok = kc + s * KS + grp * CE < kend;
             const V fb = st[i * CPR + ((s * 4 + grp) ^ i)];
-            if (s & 1) acc1 = skinny_mma<DT>(ok ? fb : zero, ok ? fa[s] : zero, acc1);
-            else acc0 = skinny_mma<DT>(ok ? fb : zero, ok ? fa[s] : zero, acc0);
+            if (s & 1) acc1 = skinny_mma<DT>(ok ? fb : zero, ok ? f[s] : zero, acc1);
+            else acc0 = skinny_mma<DT>(ok ? fb : zero, ok ? f[s] : zero, acc0);
         }
     };
     const uint32_t nch = kend > kbeg ? (kend - kbeg + KC - 1) / KC : 0;
-    if (nch > 0) {
-        load_chunk(kbeg);
-        for (uint32_t c = 0; c + 1 < nch; c++) {
+    if constexpr (DT == MX_FLOAT32) {
+        // per chunk: stage its Bt rows and load its A fragments, the next chunk's Bt loads, the MFMAs
+        if (nch > 0) load_chunk(kbeg);
+        for (uint32_t c = 0; c < nch; c++) {
             const uint32_t kc = kbeg + c * KC;
-            // issue order: stage + A loads, then the next chunk's Bt loads, then the MFMAs
-            stage_and_load_a(kc);
+            stage_b();
+            load_a(kc, fa[0]);
             __builtin_amdgcn_sched_barrier(0);
-            load_chunk(kc + KC);
+            if (c + 1 < nch) load_chunk(kc + KC);
             __builtin_amdgcn_sched_barrier(0);
-            compute(kc);
+            compute(kc, fa[0]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        const uint32_t kc = kbeg + (nch - 1) * KC;
-        stage_and_load_a(kc);
-        compute(kc);
+    } else {
+        // two chunks per turn (fa[0] holds even chunks' A, fa[1] odd ones'); per chunk: stage its Bt
+        // rows, the next chunk's Bt and A loads, the MFMAs.  Staging overwrites LDS this wave read
+        // for the last chunk (a wave's LDS accesses are in order).
+        if (nch > 0) {
+            load_chunk(kbeg);
+            load_a(kbeg, fa[0]);
+        }
+        uint32_t c = 0;
+        for (; c + 2 <= nch; c += 2) {
+            const uint32_t kc = kbeg + c * KC;
+            stage_b();
+            __builtin_amdgcn_sched_barrier(0);
+            load_chunk(kc + KC);
+            load_a(kc + KC, fa[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(kc, fa[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            stage_b();
+            __builtin_amdgcn_sched_barrier(0);
+            if (c + 2 < nch) {
+                load_chunk(kc + 2 * KC);
+                load_a(kc + 2 * KC, fa[0]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            compute(kc + KC, fa[1]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c < nch) {
+            stage_b();
+            compute(kbeg + c * KC, fa[0]);
+        }
     }
     f4v acc = acc0 + acc1;
     __shared__ f4v part[W - 1][64];
@@ -344,7 +380,7 @@ template <int DT>
 int launch_skinny(const GemmArgs& g, void* C, const void* A, const void* Bt, hipStream_t st) {
     using S = typename MmaTraits<DT>::S;
     constexpr uint32_t KS = 4 * (16 / sizeof(S));
-    constexpr int W = kSkinnyWaves;
+    constexpr int W = kSkinnyWaves<DT>;
     uint32_t kw = (g.K + W - 1) / W;
     kw = (kw + KS - 1) / KS * KS;
     bool cvec = g.cn == 1 && g.N % 4 == 0 && g.ldc % 4 == 0 && (uintptr_t)C % (4 * sizeof(S)) == 0;
