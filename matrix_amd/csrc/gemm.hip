@@ -463,8 +463,31 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
                             if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
                         return true;
                     }();
+    // A given M-major (A's K stride is its row pitch, its M stride 1: the vjp's g^T), 16-bit data:
+    // the A slot takes B's N-major layout and transposing reads, so dot() needs no copy of g^T.
+    // B either K-major (the DMA path's Bt) or N-major.
+    const bool bk = g.kb == 1 && g.ldb % CE == 0 && (uint64_t)ts.bn * g.ldb * sizeof(S) < (1ull << 32);
+    const bool bn = g.ldb == 1 && g.kb % CE == 0 && g.N % CE == 0 && 64ull * g.kb * sizeof(S) < (1ull << 32);
+    const bool amn = DT != MX_FLOAT32 && g.lda == 1 && g.ka % CE == 0 && g.M % CE == 0 &&
+                     64ull * g.ka * sizeof(S) < (1ull << 32) && (bk || bn) && (uintptr_t)A % 16 == 0 &&
+                     (uintptr_t)Bt % 16 == 0 && [&] {
+                         for (int d = 0; d < g.bd.n; d++)
+                             if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
+                         return true;
+                     }();
     const tile::MatrixSrc::Geom geo{};
     const char* who = "mx_launch_batched_matmul";
+    // the tile kernel for this layout: (K-major | M-major A) x (K-major | N-major B), or strided
+    auto tile_launch = [&](auto split, GemmArgs& ga, void* out, uint32_t ns) -> int {
+        constexpr bool SP = decltype(split)::value;
+        if constexpr (DT != MX_FLOAT32) {
+            if (amn && bn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, true, true>(ts, ga, geo, out, A, Bt, st, who, ns);
+            if (amn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, false, true>(ts, ga, geo, out, A, Bt, st, who, ns);
+        }
+        if (nn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, true>(ts, ga, geo, out, A, Bt, st, who, ns);
+        return vec ? tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc>(ts, ga, geo, out, A, Bt, st, who, ns)
+                   : tile::launch_tile_kernel<DT, false, SP, tile::MatrixSrc>(ts, ga, geo, out, A, Bt, st, who, ns);
+    };
     if (nsplit > 1 && per < 0xffffffffull) {
         // fp32 partials [split][batch][M][N] in the caller's workspace, then an ordered sum
         void* P = ws;
@@ -473,10 +496,7 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
         gp.ksplit = ksplit;
         gp.ldc = g.N;
         gp.cn = 1;
-        if (nn) rc = tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc, true>(ts, gp, geo, P, A, Bt, st, who, nsplit);
-        else
-            rc = vec ? tile::launch_tile_kernel<DT, true, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit)
-                     : tile::launch_tile_kernel<DT, false, true, tile::MatrixSrc>(ts, gp, geo, P, A, Bt, st, who, nsplit);
+        rc = tile_launch(std::true_type{}, gp, P, nsplit);
         if (rc) return rc;
         const dim3 grid((uint32_t)((per + 255) / 256));
         if (epi)
@@ -488,11 +508,7 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
         MX_HIP(hipGetLastError());
         return MX_OK;
     }
-    int rc;
-    if (nn) rc = tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc, true>(ts, g, geo, C, A, Bt, st, who);
-    else
-        rc = vec ? tile::launch_tile_kernel<DT, true, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who)
-                 : tile::launch_tile_kernel<DT, false, false, tile::MatrixSrc>(ts, g, geo, C, A, Bt, st, who);
+    const int rc = tile_launch(std::false_type{}, g, C, 1);
     return rc || !epi ? rc : launch_bias_act<DT>(g, C, *epi, st);
 }
 

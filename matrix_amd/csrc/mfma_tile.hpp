@@ -381,6 +381,32 @@ __device__ __forceinline__ void read_frags_nn16(Frags<DT, TM, WNT>& f, const cha
     }
 }
 
+// 16-bit fragments with either operand given transposed: A M-major (A as [K, M], M contiguous:
+// the vjp's g^T operand) takes the same slot layout and transposing reads as N-major B, with BM
+// for BN.
+template <int DT, int TM, int WNT, int BM, int BN, int HALF, bool AT, bool BT>
+__device__ __forceinline__ void read_frags_t16(Frags<DT, TM, WNT>& f, const char* la, const char* lb, int wm, int wn,
+                                               int lane) {
+    using V = std::remove_reference_t<decltype(f.b[0][0])>;
+    const int r32 = lane & 31, h = lane >> 5;
+    constexpr int C0 = HALF * STEP_CHUNKS;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+        for (int t = 0; t < TM; t++) {
+            const int ra = wm * (TM * 32) + t * 32 + r32;
+            if constexpr (AT) f.a[kb][t] = read_b_nn16<BM, HALF, V>(la, wm * (TM * 32) + t * 32, kb, lane);
+            else f.a[kb][t] = *reinterpret_cast<const V*>(la + ra * ROWB + swz(ra, C0 + 2 * kb + h) * 16);
+        }
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int rb = wn * (WNT * 32) + t * 32 + r32;
+            if constexpr (BT) f.b[kb][t] = read_b_nn16<BN, HALF, V>(lb, wn * (WNT * 32) + t * 32, kb, lane);
+            else f.b[kb][t] = *reinterpret_cast<const V*>(lb + rb * ROWB + swz(rb, C0 + 2 * kb + h) * 16);
+        }
+    }
+}
+
 // DMA of the 16-bit N-major B slot: one instruction fills 1 KB = 512 / BN K rows; wave w's
 // instruction i fills rows RPI (N w + i) ..; lane L lands at row RPI (N w + i) + L / (BN / 8),
 // stored chunk L % (BN / 8), so it fetches the logical chunk swz_nn16 stores there.  Columns past
@@ -617,7 +643,7 @@ __device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN 
 // (g.ldc = N, g.cn = 1), and a second kernel sums the splits in order.
 // BNN: Bt is N-major (B as [K, N]: g.ldb == 1, g.kb is B's row stride); fp32 reads it as FragsNN
 // describes, 16-bit types through transposing LDS reads (read_frags_nn16).
-template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src, bool BNN = false>
+template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src, bool BNN = false, bool AMN = false>
 __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ Cv,
                                                              const typename MmaTraits<DT>::S* __restrict__ A,
                                                              const typename MmaTraits<DT>::S* __restrict__ Bt,
@@ -679,6 +705,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
 
     constexpr bool NN32 = BNN && DT == MX_FLOAT32;      // fp32 N-major B (FragsNN)
     constexpr bool NN16 = BNN && DT != MX_FLOAT32;      // 16-bit N-major B (transposing reads)
+    static_assert(!AMN || (DT != MX_FLOAT32 && Src::kStrided), "M-major A: 16-bit matrices only");
     f16v acc[TM][WNT];
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -696,6 +723,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     auto read_step = [&](auto half, FR& f, const char* la, const char* lb) {
         constexpr int HALF = decltype(half)::value;
         if constexpr (NN32) read_frags_nn<TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
+        else if constexpr (AMN) read_frags_t16<DT, TM, WNT, BM, BN, HALF, true, NN16>(f, la, lb, wm, wn, lane);
         else if constexpr (NN16) read_frags_nn16<DT, TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
         else read_frags<DT, TM, WNT, HALF>(f, la, lb, wm, wn, lane);
     };
@@ -706,13 +734,17 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     };
     // LDS reads per step: one 16-byte read per A fragment and per K-major B fragment, two 8-byte
     // transposing reads per N-major one
-    constexpr int NREADS = 2 * (TM + (NN16 ? 2 : 1) * WNT);
+    constexpr int NREADS = 2 * ((AMN ? 2 : 1) * TM + (NN16 ? 2 : 1) * WNT);
     const auto sa = Src::template a_init<S, DMA_A>(g, geo, m0, rows_a, wave, lane);
+    // M-major A: the slot's K rows of BM elements, from the tile's first column
+    const DmaOffsets<DMA_A> oa_mn = AMN ? dma_offsets_nn16<BM, DMA_A>(rows_a, g.ka, wave, lane) : DmaOffsets<DMA_A>{};
+    const S* Amn = Abat + m0;
     const DmaOffsets<DMA_B> ob = NN32   ? dma_offsets_nn<BN, DMA_B>(rows_b, g.kb, wave, lane)
                                  : NN16 ? dma_offsets_nn16<BN, DMA_B>(rows_b, g.kb, wave, lane)
                                         : dma_offsets<S, DMA_B>(rows_b, g.ldb, wave, lane);
     auto dma_pair = [&](auto s, uint32_t p) {
-        Src::template a_dma<S, DMA_A>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
+        if constexpr (AMN) dma_rows<S, DMA_A>(slot_a(s), Amn + (uint64_t)p * 2 * KSTEP * g.ka, oa_mn, 0, wave);
+        else Src::template a_dma<S, DMA_A>(slot_a(s), Abat, sa, g, geo, m0, p, wave, lane);
         if constexpr (BNN) dma_rows<S, DMA_B>(slot_b(s), Bblk + (uint64_t)p * 2 * KSTEP * g.kb, ob, 0, wave);
         else dma_rows<S, DMA_B>(slot_b(s), Bblk, ob, p * 2 * KSTEP, wave);
     };
@@ -801,8 +833,15 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         // first half of slot 0, zero past K.
         const S* Ablk = Abat + (uint64_t)m0 * g.lda;
         for (uint32_t kt = 2 * KP; kt < KT; kt++) {
-            uint4 ra[kTailChunks<BM>];
-            load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
+            if constexpr (AMN) {
+                uint4 ra[kTailChunksNN16<BM>];
+                load_tile_guarded_nn16<BM>(ra, reinterpret_cast<const uint16_t*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
+                store_tile_nn16<BM>(la0, ra);
+            } else {
+                uint4 ra[kTailChunks<BM>];
+                load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
+                store_tile<BM>(la0, ra);
+            }
             if constexpr (NN32) {
                 f4v rb[kTailChunksNN<BN>];
                 load_tile_guarded_nn<BN>(rb, reinterpret_cast<const float*>(Bblk), rows_b, g.kb, kt * KSTEP, Klen);
@@ -816,7 +855,6 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
                 load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
                 store_tile<BN>(lb0, rb);
             }
-            store_tile<BM>(la0, ra);
             __syncthreads();
             read_step(I0{}, f0, la0, lb0);
             mma(I0{}, ITM{}, f0);
@@ -879,7 +917,7 @@ inline TileShape choose_tile(uint64_t M, uint64_t N, uint64_t batches) {
 
 // Launches mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src> for the chosen shape; with SPLIT,
 // nsplit K pieces of g.ksplit elements each.
-template <int DT, bool VEC, bool SPLIT, class Src, bool BNN = false>
+template <int DT, bool VEC, bool SPLIT, class Src, bool BNN = false, bool AMN = false>
 int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C, const void* A, const void* Bt,
                        hipStream_t st, const char* who, uint32_t nsplit = 1) {
     using S = typename MmaTraits<DT>::S;
@@ -889,7 +927,7 @@ int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C
         g.tiles_n = (g.N + BN - 1) / BN;
         const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches * nsplit;
         if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": grid too large");
-        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src, BNN>), dim3((uint32_t)blocks),
+        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src, BNN, AMN>), dim3((uint32_t)blocks),
                            dim3(NTHREADS), 0, st, C, (const S*)A, (const S*)Bt, g, geo);
         MX_HIP(hipGetLastError());
         return MX_OK;

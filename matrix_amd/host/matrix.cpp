@@ -930,8 +930,22 @@ static bool n_major_ok(const matrix& a, const matrix& bt) {
     return rows > 16;
 }
 
+// A 16-bit A given M-major (a transposed view whose M axis is unit-stride, the vjp's g^T) that
+// the tile kernel reads through transposing LDS reads: 16-byte K rows, M a whole number of them.
+static bool m_major_ok(const matrix& a) {
+    if ((a.type != dtype::Float16 && a.type != dtype::BFloat16) || a.dims < 2) return false;
+    const uint32_t ce = 8;
+    const size_m* st = a.strides();
+    const size_m* sh = a.shape();
+    if (st[a.dims - 2] != 1 || st[a.dims - 1] % ce || sh[a.dims - 2] % ce || a.offset % ce) return false;
+    for (uint32_t d = 0; d + 2 < a.dims; d++)
+        if (sh[d] > 1 && st[d] % ce) return false;
+    return true;
+}
+
 // dot packs B^T contiguous (and A when it is a strided view) before the product, as the
-// reference does (Matrix.mm:7068-7092) -- except a float B that is already N-major.
+// reference does (Matrix.mm:7068-7092) -- except a float B that is already N-major and a 16-bit
+// A that is M-major.
 matrix matrix::dot(const matrix& b, bool transposeB) const {
     if (dims < 2 || b.dims < 2) throw std::invalid_argument("matrix::dot requires both matrices to be at least 2D");
     require_real(type, "dot");
@@ -944,7 +958,7 @@ matrix matrix::dot(const matrix& b, bool transposeB) const {
         bt = b.transpose(axes);
     }
     if (!bt.is_contiguous() && !(bt.type == type && n_major_ok(*this, bt))) bt = bt.astype(bt.type, true);
-    matrix a = is_contiguous() ? *this : astype(type, true);
+    matrix a = is_contiguous() || m_major_ok(*this) ? *this : astype(type, true);
     if (bt.type != a.type) bt = bt.astype(a.type, true);
     uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];
     if (mx_broadcast_shapes_matmul(a.shape(), a.strides(), a.dims, bt.shape(), bt.strides(), bt.dims, os, ost, b1s, b1t,

@@ -98,7 +98,16 @@ CASE(shapes_dot_and_conv) {
         EXPECT(c16.tape->input_at(1).storage == b16.storage, "16-bit N-major B is not copied");
         matrix c40 = matrix::leaf({64, 32}, t).dot(matrix::leaf({32, 44}, t));
         EXPECT(c40.tape->input_at(1).is_contiguous(), "16-bit N not a multiple of 8: B^T is packed");
+        // the vjp's g^T . A: g^T is an M-major view of g, read without a copy
+        matrix g16 = matrix::leaf({64, 48}, t);
+        matrix gt = g16.transpose({1, 0}).dot(matrix::leaf({64, 32}, t));
+        EXPECT(gt.tape->input_at(0).storage == g16.storage, "16-bit M-major A is not copied");
+        matrix gt44 = matrix::leaf({64, 44}, t).transpose({1, 0}).dot(matrix::leaf({64, 32}, t));
+        EXPECT(gt44.tape->input_at(0).is_contiguous(), "16-bit M not a multiple of 8: A is packed");
     }
+    matrix g32 = matrix::leaf({64, 48});
+    EXPECT(g32.transpose({1, 0}).dot(matrix::leaf({64, 32})).tape->input_at(0).is_contiguous(),
+           "fp32 M-major A is packed");
     matrix cs = matrix::leaf({8, 1, 32}).dot(matrix::leaf({32, 48}));
     EXPECT(cs.tape->input_at(1).is_contiguous(), "fp32, at most 16 rows of A (the streaming kernel): B^T is packed");
     matrix c10 = a.dot(matrix::leaf({32, 10}));
@@ -734,6 +743,45 @@ CASE(gpu_complex64_arithmetic) {
         }
 }
 
+// An f16 dense layer's weight gradient: loss = (x . W).sum(), so dL/dW = x^T . 1 and the Dot's
+// vjp forms g^T . x, whose g^T is read M-major (no copy); against float64 host sums of the same
+// f16 inputs (each output a sum of 64 products; f16 result rounding).
+CASE(gpu_f16_dot_vjp) {
+    const size_m M = 64, K = 96, N = 128;
+    auto xf = randn((size_t)M * K, 80), wf = randn((size_t)K * N, 81, 0.1f);
+    std::vector<_Float16> xh(xf.size()), wh(wf.size());
+    for (size_t i = 0; i < xf.size(); i++) xh[i] = (_Float16)xf[i];
+    for (size_t i = 0; i < wf.size(); i++) wh[i] = (_Float16)wf[i];
+    matrix x = matrix::from_host<_Float16>({M, K}, xh);
+    matrix W = matrix::from_host<_Float16>({K, N}, wh);
+    matrix y = x.dot(W);
+    matrix t = matrix::from_host<_Float16>({M, N}, std::vector<_Float16>((size_t)M * N, (_Float16)0.25f));
+    matrix loss = (y * t).sum();
+    std::vector<matrix> outs{loss}, params{W, x};
+    std::vector<matrix> grads = matrix::build_grad_graph(outs, params);
+    matrix::eval(grads);
+    auto gw = grads[0].to_host<_Float16>();
+    auto gx = grads[1].to_host<_Float16>();
+    double err = 0, mag = 0;
+    for (size_t k = 0; k < K; k++)
+        for (size_t n = 0; n < N; n++) {
+            double ref = 0;                     // dL/dW[k, n] = sum_m x[m, k] * 0.25
+            for (size_t m = 0; m < M; m++) ref += 0.25 * (double)(float)xh[m * K + k];
+            err += ((double)(float)gw[k * N + n] - ref) * ((double)(float)gw[k * N + n] - ref);
+            mag += ref * ref;
+        }
+    EXPECT(std::sqrt(err / mag) <= 2e-3, "f16 weight gradient (g^T . x) beyond 2e-3 normwise");
+    err = mag = 0;
+    for (size_t m = 0; m < M; m++)
+        for (size_t k = 0; k < K; k++) {
+            double ref = 0;                     // dL/dx[m, k] = sum_n 0.25 * W[k, n]
+            for (size_t n = 0; n < N; n++) ref += 0.25 * (double)(float)wh[k * N + n];
+            err += ((double)(float)gx[m * K + k] - ref) * ((double)(float)gx[m * K + k] - ref);
+            mag += ref * ref;
+        }
+    EXPECT(std::sqrt(err / mag) <= 2e-3, "f16 input gradient (g . W^T) beyond 2e-3 normwise");
+}
+
 int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "cpu";
     if (mode == "cpu") {
@@ -753,6 +801,7 @@ int main(int argc, char** argv) {
         run("gpu_mlp_training_step_compile_once", gpu_mlp_training_step_compile_once);
         run("gpu_value_and_grad", gpu_value_and_grad);
         run("gpu_complex64_arithmetic", gpu_complex64_arithmetic);
+        run("gpu_f16_dot_vjp", gpu_f16_dot_vjp);
     }
     return g_fail ? 1 : 0;
 }

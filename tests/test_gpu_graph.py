@@ -18,4 +18,4 @@ def test_graph_on_gpu():
     out = subprocess.run([str(BIN), "gpu"], capture_output=True, text=True, timeout=110)
     print(out.stdout)
     assert out.returncode == 0, out.stdout + out.stderr
-    assert "FAIL" not in out.stdout and out.stdout.count("PASS") == 10, out.stdout
+    assert "FAIL" not in out.stdout and out.stdout.count("PASS") == 11, out.stdout

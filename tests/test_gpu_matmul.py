@@ -12,7 +12,7 @@ import math
 import numpy as np
 import pytest
 
-from helpers import contiguous_strides, normwise_rel
+from helpers import bits, contiguous_strides, normwise_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -341,3 +341,68 @@ def test_n_major_b_one_hot_exact(mx, orc, dt, MKN):
     b = gen(rng, code, [K, N], 1.0, mx)
     got, _, _ = run_mm(mx, orc, code, a, b, bt_shape=[N, K], bt_strides=[1, N], oracle=False)
     assert np.array_equal(got.reshape(M, N), b[ks])
+
+
+@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("b_nmajor", [False, True])
+@pytest.mark.parametrize("case", [
+    ([2, 200, 304], [2, 200, 152]),      # A^T [.., K, M]: ragged M (multiple of 8), K tail, per-batch B
+    ([1024, 512], [1024, 4096]),         # g^T . A of the MLP's first layer shape: split K
+    ([96, 4096], [96, 4096]),            # 256 x 256 tiles, K a single pair and a half
+    ([3000, 64], [3000, 72]),            # long ragged K: split K, short last split
+    ([64, 44], [64, 32]),                # M not a multiple of 8: the strided fallback
+])
+def test_m_major_a(mx, orc, dt, b_nmajor, case):
+    """A handed over M-major (a transposed view of A^T stored [..., K, M], the vjp's g^T):
+    16-bit types read it through transposing LDS reads.  The result must equal the same product
+    on the packed A bit for bit (the fragments are the same), and the oracle / fp64 within the
+    usual bounds."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(19)
+    at_shape, b_shape = case
+    K, M, N = at_shape[-2], at_shape[-1], b_shape[-1]
+    at = gen(rng, code, at_shape, 1.0 / math.sqrt(K), mx)
+    b = gen(rng, code, b_shape, 1.0, mx)
+    ast = contiguous_strides(at_shape)
+    a_shape = at_shape[:-2] + [M, K]
+    a_strides = ast[:-2] + [1, M]
+    bst = contiguous_strides(b_shape)
+    bt_shape = b_shape[:-2] + [N, K]
+    if b_nmajor:
+        bt_store, bt_strides = b, bst[:-2] + [1, N]
+    else:
+        bt_store = np.ascontiguousarray(np.swapaxes(b, -1, -2))
+        bt_strides = contiguous_strides(bt_shape)
+    got, _, out = run_mm(mx, orc, code, at, bt_store, a_shape=a_shape, a_strides=a_strides, bt_shape=bt_shape,
+                         bt_strides=bt_strides, oracle=False)
+    a = np.ascontiguousarray(np.swapaxes(at, -1, -2))
+    packed, _, _ = run_mm(mx, orc, code, a, bt_store, bt_shape=bt_shape, bt_strides=bt_strides, oracle=False)
+    if M % 8 == 0:                        # the transposed slot: the very fragments of the packed A
+        assert np.array_equal(bits(got), bits(packed)), "M-major A differs from the packed A"
+    bt = np.ascontiguousarray(np.swapaxes(b, -1, -2))
+    _, desc = matmul_desc(mx, list(a.shape), contiguous_strides(list(a.shape)), list(bt.shape),
+                          contiguous_strides(list(bt.shape)))
+    ref = orc.batched_matmul(code, desc, K, a.reshape(-1), bt.reshape(-1), int(np.prod(out)), acc=orc.ACC_F32)
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
+    ref64 = np.matmul(as_f32(code, a, mx).astype(np.float64), as_f32(code, b, mx).astype(np.float64))
+    assert normwise_rel(as_f32(code, got, mx), ref64.reshape(-1)) <= NN_TOL64[dt]
+
+
+@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("MKN", [(304, 200, 152), (1024, 256, 512), (256, 64, 256)])
+def test_m_major_a_one_hot_exact(mx, orc, dt, MKN):
+    """One-hot rows of an M-major A pick B rows exactly: C[m, :] = B[k_m, :] (the rows and K rows of
+    the transposed A slot and the epilogue's placement)."""
+    code = getattr(mx, dt)
+    M, K, N = MKN
+    rng = np.random.default_rng(20)
+    ks = rng.integers(0, K, M)
+    one = np.float16(1.0).view(np.uint16) if code == mx.FLOAT16 else np.uint16(0x3F80)
+    at = np.zeros([K, M], np.uint16)
+    at[ks, np.arange(M)] = one
+    if code == mx.FLOAT16:
+        at = at.view(np.float16)
+    b = gen(rng, code, [K, N], 1.0, mx)
+    bt = np.ascontiguousarray(b.T)
+    got, _, _ = run_mm(mx, orc, code, at, bt, a_shape=[M, K], a_strides=[1, M], oracle=False)
+    assert np.array_equal(bits(got.reshape(M, N)), bits(b[ks]))
