@@ -463,12 +463,12 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
                             if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
                         return true;
                     }();
-    // A given M-major (A's K stride is its row pitch, its M stride 1: the vjp's g^T), 16-bit data:
-    // the A slot takes B's N-major layout and transposing reads, so dot() needs no copy of g^T.
-    // B either K-major (the DMA path's Bt) or N-major.
+    // A given M-major (A's K stride is its row pitch, its M stride 1: the vjp's g^T): the A slot
+    // takes B's N-major layout (16-bit: transposing reads; fp32: Frags32T), so dot() needs no copy
+    // of g^T.  B either K-major (the DMA path's Bt) or N-major.
     const bool bk = g.kb == 1 && g.ldb % CE == 0 && (uint64_t)ts.bn * g.ldb * sizeof(S) < (1ull << 32);
     const bool bn = g.ldb == 1 && g.kb % CE == 0 && g.N % CE == 0 && 64ull * g.kb * sizeof(S) < (1ull << 32);
-    const bool amn = DT != MX_FLOAT32 && g.lda == 1 && g.ka % CE == 0 && g.M % CE == 0 &&
+    const bool amn = g.lda == 1 && g.ka % CE == 0 && g.M % CE == 0 &&
                      64ull * g.ka * sizeof(S) < (1ull << 32) && (bk || bn) && (uintptr_t)A % 16 == 0 &&
                      (uintptr_t)Bt % 16 == 0 && [&] {
                          for (int d = 0; d < g.bd.n; d++)
@@ -480,10 +480,8 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
     // the tile kernel for this layout: (K-major | M-major A) x (K-major | N-major B), or strided
     auto tile_launch = [&](auto split, GemmArgs& ga, void* out, uint32_t ns) -> int {
         constexpr bool SP = decltype(split)::value;
-        if constexpr (DT != MX_FLOAT32) {
-            if (amn && bn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, true, true>(ts, ga, geo, out, A, Bt, st, who, ns);
-            if (amn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, false, true>(ts, ga, geo, out, A, Bt, st, who, ns);
-        }
+        if (amn && bn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, true, true>(ts, ga, geo, out, A, Bt, st, who, ns);
+        if (amn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, false, true>(ts, ga, geo, out, A, Bt, st, who, ns);
         if (nn) return tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc, true>(ts, ga, geo, out, A, Bt, st, who, ns);
         return vec ? tile::launch_tile_kernel<DT, true, SP, tile::MatrixSrc>(ts, ga, geo, out, A, Bt, st, who, ns)
                    : tile::launch_tile_kernel<DT, false, SP, tile::MatrixSrc>(ts, ga, geo, out, A, Bt, st, who, ns);

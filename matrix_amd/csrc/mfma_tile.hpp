@@ -245,6 +245,66 @@ __device__ __forceinline__ void mma_step_nn(f16v (&acc)[TM][WNT], const FragsNN<
                 acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.b[s][q], f4_at(f.a[0][i], s), acc[i][q], 0, 0, 0);
 }
 
+// fp32 with A M-major (A as [K, M], M contiguous: the vjp's g^T), and B K- or N-major.  The A slot
+// holds the pair's 32 K rows of BM floats, read like the N-major B slot: lane (i = l % 32, h)
+// loads, for substep s, row 8 h + s and rows TM i .. TM i + TM - 1 of the wave's A range, and the
+// MFMA of A tile t takes element t -- so accumulator t holds C row TM (l % 32) + t of the wave's
+// range (the epilogue maps rows accordingly) instead of 32 t + l % 32.
+template <int TM, int WNT, bool BT> struct Frags32T {
+    static constexpr int KB = 1;
+    typedef float avec __attribute__((ext_vector_type(TM)));
+    typedef float bvec __attribute__((ext_vector_type(WNT)));
+    avec a[8];
+    f4v bk[1][WNT][2];                     // B K-major (BT false)
+    bvec bn[8];                            // B N-major (BT true)
+};
+
+template <int TM, int WNT, int BM, int BN, int HALF, bool BT>
+__device__ __forceinline__ void read_frags_32t(Frags32T<TM, WNT, BT>& f, const char* la, const char* lb, int wm, int wn,
+                                               int lane) {
+    using AV = typename Frags32T<TM, WNT, BT>::avec;
+    using BV = typename Frags32T<TM, WNT, BT>::bvec;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int acol = wm * (TM * 32) + TM * r32;
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const int row = HALF * 16 + 8 * h + s;
+        f.a[s] = *reinterpret_cast<const AV*>(la + row * (BM * 4) + acol * 4);
+    }
+    if constexpr (BT) {
+        const int col = wn * (WNT * 32) + WNT * r32;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const int row = HALF * 16 + 8 * h + s;
+            f.bn[s] = *reinterpret_cast<const BV*>(lb + row * (BN * 4) + col * 4);
+        }
+    } else {
+        constexpr int C0 = HALF * STEP_CHUNKS;
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int rb = wn * (WNT * 32) + t * 32 + r32;
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+                f.bk[0][t][u] = *reinterpret_cast<const f4v*>(lb + rb * ROWB + swz(rb, C0 + 2 * h + u) * 16);
+        }
+    }
+}
+
+template <int TM, int WNT, int I0, int I1, bool BT>
+__device__ __forceinline__ void mma_step_32t(f16v (&acc)[TM][WNT], const Frags32T<TM, WNT, BT>& f) {
+#pragma unroll
+    for (int s = 0; s < 8; s++)
+#pragma unroll
+        for (int i = I0; i < I1; i++)
+#pragma unroll
+            for (int q = 0; q < WNT; q++) {
+                if constexpr (BT)
+                    acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.bn[s][q], f.a[s][i], acc[i][q], 0, 0, 0);
+                else
+                    acc[i][q] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4_at(f.bk[0][q], s), f.a[s][i], acc[i][q], 0, 0, 0);
+            }
+}
+
 // Direct global -> LDS copy of one operand's K pair (two steps, 128 bytes of each row -- whole
 // L2 lines).  Each of a wave's DMA instructions fills 1 KB = 8 LDS rows; lane L lands at row
 // r = 8 p + L / 8, stored chunk L % 8, so it fetches the logical chunk that swz() stores there
@@ -535,12 +595,14 @@ __device__ __forceinline__ void ring_barrier() {
 // row bytes.  The quarter is written to LDS whole (16-byte chunk c of row r at
 // c ^ (r mod chunks per row)), then read back and stored row-major.  Otherwise an interior tile
 // stores 4 columns per instruction from the fragments, and other tiles one element at a time.
-template <int DT, int BM, int BN, bool SPLIT, class Src, bool STAGE, typename CT>
+template <int DT, int BM, int BN, bool SPLIT, class Src, bool STAGE, typename CT, bool RT = false>
 __device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN / 64], const GemmArgs& g,
                                         const typename Src::Geom& geo, uint32_t m0, uint32_t n0, int wm, int wn, int lane,
                                         bool vec_store, char* stage) {
     constexpr int TM = BM / 64, WNT = BN / 64;
     const int h = lane >> 5, c32 = lane & 31;
+    // row of accumulator tile i within the wave's range (RT: fp32 M-major A, Frags32T)
+    auto rin = [&](int i) { return RT ? TM * c32 + i : i * 32 + c32; };
     auto cvt = [](float v) -> CT {
         if constexpr (SPLIT || DT == MX_FLOAT32) return v;
         else if constexpr (DT == MX_FLOAT16) return float_to_half_bits(v);
@@ -555,7 +617,7 @@ __device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN 
             static_assert((CPRS & (CPRS - 1)) == 0 && CPRS <= 32, "staged row chunks");
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                const int r = i * 32 + c32;
+                const int r = rin(i);
 #pragma unroll
                 for (int j = 0; j < WNT; j++)
 #pragma unroll
@@ -592,7 +654,7 @@ __device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN 
     if (interior) {                                           // 4 columns per store
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-            const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+            const uint32_t row = m0 + wm * (TM * 32) + rin(i);
             CT* crow = Cbat + Src::row_off(g, geo, row) + n0 + wn * (WNT * 32) + 4 * h;
 #pragma unroll
             for (int j = 0; j < WNT; j++)
@@ -614,7 +676,7 @@ __device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN 
     }
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+        const uint32_t row = m0 + wm * (TM * 32) + rin(i);
         if (row >= g.M) continue;
         CT* crow = Cbat + Src::row_off(g, geo, row);
 #pragma unroll
@@ -705,7 +767,8 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
 
     constexpr bool NN32 = BNN && DT == MX_FLOAT32;      // fp32 N-major B (FragsNN)
     constexpr bool NN16 = BNN && DT != MX_FLOAT32;      // 16-bit N-major B (transposing reads)
-    static_assert(!AMN || (DT != MX_FLOAT32 && Src::kStrided), "M-major A: 16-bit matrices only");
+    static_assert(!AMN || Src::kStrided, "M-major A: matrices only");
+    constexpr bool T32 = AMN && DT == MX_FLOAT32;        // fp32 M-major A (Frags32T, rows remapped)
     f16v acc[TM][WNT];
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -718,18 +781,21 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     const uint32_t KP = VEC ? Klen / (2 * KSTEP) : 0;  // whole K pairs copied by LDS DMA
     // Fragments are double-buffered in registers: f0 holds a pair's first step, f1 its second;
     // each step reads the next step's fragments while its own MFMAs run.
-    using FR = std::conditional_t<NN32, FragsNN<TM, WNT>, Frags<DT, TM, WNT>>;
+    using FR = std::conditional_t<T32, Frags32T<TM, WNT, BNN>,
+                                  std::conditional_t<NN32, FragsNN<TM, WNT>, Frags<DT, TM, WNT>>>;
     FR f0, f1;
     auto read_step = [&](auto half, FR& f, const char* la, const char* lb) {
         constexpr int HALF = decltype(half)::value;
-        if constexpr (NN32) read_frags_nn<TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
+        if constexpr (T32) read_frags_32t<TM, WNT, BM, BN, HALF, BNN>(f, la, lb, wm, wn, lane);
+        else if constexpr (NN32) read_frags_nn<TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
         else if constexpr (AMN) read_frags_t16<DT, TM, WNT, BM, BN, HALF, true, NN16>(f, la, lb, wm, wn, lane);
         else if constexpr (NN16) read_frags_nn16<DT, TM, WNT, BN, HALF>(f, la, lb, wm, wn, lane);
         else read_frags<DT, TM, WNT, HALF>(f, la, lb, wm, wn, lane);
     };
     auto mma = [&](auto i0, auto i1, const FR& f) {
         constexpr int I0_ = decltype(i0)::value, I1_ = decltype(i1)::value;
-        if constexpr (NN32) mma_step_nn<TM, WNT, I0_, I1_>(acc, f);
+        if constexpr (T32) mma_step_32t<TM, WNT, I0_, I1_, BNN>(acc, f);
+        else if constexpr (NN32) mma_step_nn<TM, WNT, I0_, I1_>(acc, f);
         else mma_step<DT, TM, WNT, I0_, I1_>(acc, f);
     };
     // LDS reads per step: one 16-byte read per A fragment and per K-major B fragment, two 8-byte
@@ -737,7 +803,9 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     constexpr int NREADS = 2 * ((AMN ? 2 : 1) * TM + (NN16 ? 2 : 1) * WNT);
     const auto sa = Src::template a_init<S, DMA_A>(g, geo, m0, rows_a, wave, lane);
     // M-major A: the slot's K rows of BM elements, from the tile's first column
-    const DmaOffsets<DMA_A> oa_mn = AMN ? dma_offsets_nn16<BM, DMA_A>(rows_a, g.ka, wave, lane) : DmaOffsets<DMA_A>{};
+    const DmaOffsets<DMA_A> oa_mn = !AMN ? DmaOffsets<DMA_A>{}
+                                    : T32 ? dma_offsets_nn<BM, DMA_A>(rows_a, g.ka, wave, lane)
+                                          : dma_offsets_nn16<BM, DMA_A>(rows_a, g.ka, wave, lane);
     const S* Amn = Abat + m0;
     const DmaOffsets<DMA_B> ob = NN32   ? dma_offsets_nn<BN, DMA_B>(rows_b, g.kb, wave, lane)
                                  : NN16 ? dma_offsets_nn16<BN, DMA_B>(rows_b, g.kb, wave, lane)
@@ -833,7 +901,11 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         // first half of slot 0, zero past K.
         const S* Ablk = Abat + (uint64_t)m0 * g.lda;
         for (uint32_t kt = 2 * KP; kt < KT; kt++) {
-            if constexpr (AMN) {
+            if constexpr (T32) {
+                f4v ra[kTailChunksNN<BM>];
+                load_tile_guarded_nn<BM>(ra, reinterpret_cast<const float*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
+                store_tile_nn<BM>(la0, ra);
+            } else if constexpr (AMN) {
                 uint4 ra[kTailChunksNN16<BM>];
                 load_tile_guarded_nn16<BM>(ra, reinterpret_cast<const uint16_t*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
                 store_tile_nn16<BM>(la0, ra);
@@ -862,8 +934,8 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         }
     }
 
-    // epilogue: acc[i][j][4 q + e] is C[row, col] with row = 32 i + lane % 32 and
-    // col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
+    // epilogue: acc[i][j][4 q + e] is C[row, col] with row = 32 i + lane % 32 (fp32 M-major A:
+    // TM (lane % 32) + i) and col = 32 j + 8 q + 4 (lane / 32) + e (the C^T fragment, see mma_step)
     CT* Cbat = static_cast<CT*>(Cv) + offC;
     const int h = lane >> 5, c32 = lane & 31;
     const bool vec_store = g.cn == 1 && Src::template row_vec_ok<CT>(g, geo) && ((uintptr_t)Cbat % 16) == 0;
@@ -875,7 +947,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         const bool interior = m0 + BM <= g.M && n0 + BN <= g.N && vec_store;
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-            const uint32_t row = m0 + wm * (TM * 32) + i * 32 + c32;
+            const uint32_t row = m0 + wm * (TM * 32) + (T32 ? TM * c32 + i : i * 32 + c32);
             if (!interior && row >= g.M) continue;
             CT* crow = Cbat + Src::row_off(g, geo, row);
 #pragma unroll
@@ -899,7 +971,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     // every wave has passed the barrier after its last fragment reads)
     constexpr bool STAGE = (BM / 2) * (BN / 2) * (int)sizeof(CT) <= (SLOT_A < SLOT_B ? SLOT_A : SLOT_B);
     char* stage = wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? lb0 : lb1;
-    store_c<DT, BM, BN, SPLIT, Src, STAGE>(Cbat, acc, g, geo, m0, n0, wm, wn, lane, vec_store, stage);
+    store_c<DT, BM, BN, SPLIT, Src, STAGE, CT, T32>(Cbat, acc, g, geo, m0, n0, wm, wn, lane, vec_store, stage);
 }
 
 // Tile shape for a problem: 256 x 256 tiles while they give at least one block per CU (256), 256 x

@@ -930,11 +930,11 @@ static bool n_major_ok(const matrix& a, const matrix& bt) {
     return rows > 16;
 }
 
-// A 16-bit A given M-major (a transposed view whose M axis is unit-stride, the vjp's g^T) that
-// the tile kernel reads through transposing LDS reads: 16-byte K rows, M a whole number of them.
+// A float A given M-major (a transposed view whose M axis is unit-stride, the vjp's g^T) that the
+// tile kernel reads from an M-major slot: 16-byte K rows, M a whole number of 16-byte units.
 static bool m_major_ok(const matrix& a) {
-    if ((a.type != dtype::Float16 && a.type != dtype::BFloat16) || a.dims < 2) return false;
-    const uint32_t ce = 8;
+    if (!is_floating(a.type) || a.dims < 2) return false;
+    const uint32_t ce = 16 / (uint32_t)dtype_size(a.type);
     const size_m* st = a.strides();
     const size_m* sh = a.shape();
     if (st[a.dims - 2] != 1 || st[a.dims - 1] % ce || sh[a.dims - 2] % ce || a.offset % ce) return false;
@@ -944,8 +944,8 @@ static bool m_major_ok(const matrix& a) {
 }
 
 // dot packs B^T contiguous (and A when it is a strided view) before the product, as the
-// reference does (Matrix.mm:7068-7092) -- except a float B that is already N-major and a 16-bit
-// A that is M-major.
+// reference does (Matrix.mm:7068-7092) -- except a float B that is already N-major and a float A
+// that is M-major.
 matrix matrix::dot(const matrix& b, bool transposeB) const {
     if (dims < 2 || b.dims < 2) throw std::invalid_argument("matrix::dot requires both matrices to be at least 2D");
     require_real(type, "dot");

@@ -106,8 +106,10 @@ CASE(shapes_dot_and_conv) {
         EXPECT(gt44.tape->input_at(0).is_contiguous(), "16-bit M not a multiple of 8: A is packed");
     }
     matrix g32 = matrix::leaf({64, 48});
-    EXPECT(g32.transpose({1, 0}).dot(matrix::leaf({64, 32})).tape->input_at(0).is_contiguous(),
-           "fp32 M-major A is packed");
+    EXPECT(g32.transpose({1, 0}).dot(matrix::leaf({64, 32})).tape->input_at(0).storage == g32.storage,
+           "fp32 M-major A is not copied");
+    EXPECT(matrix::leaf({64, 42}).transpose({1, 0}).dot(matrix::leaf({64, 32})).tape->input_at(0).is_contiguous(),
+           "fp32 M not a multiple of 4: A is packed");
     matrix cs = matrix::leaf({8, 1, 32}).dot(matrix::leaf({32, 48}));
     EXPECT(cs.tape->input_at(1).is_contiguous(), "fp32, at most 16 rows of A (the streaming kernel): B^T is packed");
     matrix c10 = a.dot(matrix::leaf({32, 10}));

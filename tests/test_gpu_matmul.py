@@ -343,7 +343,7 @@ def test_n_major_b_one_hot_exact(mx, orc, dt, MKN):
     assert np.array_equal(got.reshape(M, N), b[ks])
 
 
-@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
 @pytest.mark.parametrize("b_nmajor", [False, True])
 @pytest.mark.parametrize("case", [
     ([2, 200, 304], [2, 200, 152]),      # A^T [.., K, M]: ragged M (multiple of 8), K tail, per-batch B
@@ -354,9 +354,9 @@ def test_n_major_b_one_hot_exact(mx, orc, dt, MKN):
 ])
 def test_m_major_a(mx, orc, dt, b_nmajor, case):
     """A handed over M-major (a transposed view of A^T stored [..., K, M], the vjp's g^T):
-    16-bit types read it through transposing LDS reads.  The result must equal the same product
-    on the packed A bit for bit (the fragments are the same), and the oracle / fp64 within the
-    usual bounds."""
+    16-bit types read it through transposing LDS reads, fp32 through its own fragment layout.  The
+    16-bit result must equal the same product on the packed A bit for bit (the fragments are the
+    same); every result matches the oracle / fp64 within the usual bounds."""
     code = getattr(mx, dt)
     rng = np.random.default_rng(19)
     at_shape, b_shape = case
@@ -377,7 +377,7 @@ def test_m_major_a(mx, orc, dt, b_nmajor, case):
                          bt_strides=bt_strides, oracle=False)
     a = np.ascontiguousarray(np.swapaxes(at, -1, -2))
     packed, _, _ = run_mm(mx, orc, code, a, bt_store, bt_shape=bt_shape, bt_strides=bt_strides, oracle=False)
-    if M % 8 == 0:                        # the transposed slot: the very fragments of the packed A
+    if M % 8 == 0 and code != mx.FLOAT32:   # the transposed slot: the very fragments of the packed A
         assert np.array_equal(bits(got), bits(packed)), "M-major A differs from the packed A"
     bt = np.ascontiguousarray(np.swapaxes(b, -1, -2))
     _, desc = matmul_desc(mx, list(a.shape), contiguous_strides(list(a.shape)), list(bt.shape),
@@ -388,8 +388,8 @@ def test_m_major_a(mx, orc, dt, b_nmajor, case):
     assert normwise_rel(as_f32(code, got, mx), ref64.reshape(-1)) <= NN_TOL64[dt]
 
 
-@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
-@pytest.mark.parametrize("MKN", [(304, 200, 152), (1024, 256, 512), (256, 64, 256)])
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("MKN", [(304, 200, 152), (1024, 256, 512), (256, 64, 256), (4096, 64, 4096)])
 def test_m_major_a_one_hot_exact(mx, orc, dt, MKN):
     """One-hot rows of an M-major A pick B rows exactly: C[m, :] = B[k_m, :] (the rows and K rows of
     the transposed A slot and the epilogue's placement)."""
@@ -397,11 +397,15 @@ def test_m_major_a_one_hot_exact(mx, orc, dt, MKN):
     M, K, N = MKN
     rng = np.random.default_rng(20)
     ks = rng.integers(0, K, M)
-    one = np.float16(1.0).view(np.uint16) if code == mx.FLOAT16 else np.uint16(0x3F80)
-    at = np.zeros([K, M], np.uint16)
-    at[ks, np.arange(M)] = one
-    if code == mx.FLOAT16:
-        at = at.view(np.float16)
+    if code == mx.FLOAT32:
+        at = np.zeros([K, M], np.float32)
+        at[ks, np.arange(M)] = 1.0
+    else:
+        one = np.float16(1.0).view(np.uint16) if code == mx.FLOAT16 else np.uint16(0x3F80)
+        at = np.zeros([K, M], np.uint16)
+        at[ks, np.arange(M)] = one
+        if code == mx.FLOAT16:
+            at = at.view(np.float16)
     b = gen(rng, code, [K, N], 1.0, mx)
     bt = np.ascontiguousarray(b.T)
     got, _, _ = run_mm(mx, orc, code, at, bt, a_shape=[M, K], a_strides=[1, M], oracle=False)
