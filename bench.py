@@ -291,10 +291,9 @@ def matmul_case(mx, dt, kind, rng):
 
 
 def matmul_graph_case(mx, dt, kind, rng):
-    """launch(i) of config 3's product as the graph's A.dot(B) runs it from B stored [K, N]: the
-    tile kernel reads B N-major (no copy), except for the fp32 skinny product (8 rows of A), for
-    which dot() packs B^T with the strided copy and runs the streaming kernel on it (both launches
-    timed)."""
+    """launch(i) of config 3's product as the graph's A.dot(B) runs it from B stored [K, N], with
+    no transposed copy of B: the tile kernel (main) or the streaming kernel (skinny, 8 rows of A)
+    reads B N-major."""
     code = mx.FLOAT32 if dt == "f32" else mx.FLOAT16
     if kind == "main":
         a = _normal(rng, [16, 2048, 2048], 1 / np.sqrt(2048), dt)
@@ -307,24 +306,14 @@ def matmul_graph_case(mx, dt, kind, rng):
     A = mx.DeviceBuffer.from_numpy(a)
     Bs = [mx.DeviceBuffer.from_numpy(b) for _ in range(copies)]
     C = mx.DeviceBuffer(batch * M * N * a.itemsize)
-    if kind == "main" or dt != "f32":
-        desc = ([batch, M, N], [M * K, K, 1], [0, 1, N], [M * N, N, 1])      # Bt = B^T as a view
-        wsb = mx.matmul_workspace_bytes(code, desc, K)
-        W = mx.DeviceBuffer(wsb) if wsb else None
-        mm = mx.prepare_batched_matmul(code, desc, K, workspace=W.ptr if W else 0, workspace_bytes=wsb)
-
-        def launch(i=0):
-            mm(C.ptr, A.ptr, Bs[i % copies].ptr)
-        launch.keep = (A, Bs, C, W)
-        return launch
-    Bt = mx.DeviceBuffer(K * N * a.itemsize)
-    desc = ([batch, M, N], [M * K, K, 1], [0, K, 1], [M * N, N, 1])
-    mm = mx.prepare_batched_matmul(code, desc, K)
+    desc = ([batch, M, N], [M * K, K, 1], [0, 1, N], [M * N, N, 1])          # Bt = B^T as a view
+    wsb = mx.matmul_workspace_bytes(code, desc, K)
+    W = mx.DeviceBuffer(wsb) if wsb else None
+    mm = mx.prepare_batched_matmul(code, desc, K, workspace=W.ptr if W else 0, workspace_bytes=wsb)
 
     def launch(i=0):
-        mx.launch_copy_strided(code, code, ([N, K], [K, 1], [1, N]), Bt.ptr, Bs[i % copies].ptr)
-        mm(C.ptr, A.ptr, Bt.ptr)
-    launch.keep = (A, Bs, C, Bt)
+        mm(C.ptr, A.ptr, Bs[i % copies].ptr)
+    launch.keep = (A, Bs, C, W)
     return launch
 
 
@@ -361,9 +350,8 @@ def config_matmul(mx):
         ms = _timed(mx, launch, 40)
         gbs = nbytes / (ms * 1e-3) / 1e9
         res[f"skinny_{dt}_dot"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                                   "note": ("B stored [K, N]: the B^T copy plus the streaming kernel" if dt == "f32" else
-                                            "B stored [K, N], read N-major by the tile kernel (split K)") +
-                                           "; GB/s over the product's A + B + C bytes"}
+                                   "note": "B stored [K, N], read N-major by the streaming kernel (no transposed "
+                                           "copy); GB/s over the product's A + B + C bytes"}
         del launch
     res["_cpu_inputs"] = cpu_in
     return res

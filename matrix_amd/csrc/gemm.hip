@@ -88,18 +88,18 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(typename MmaTraits<DT>:
     const uint64_t per = (uint64_t)g.batches * g.M * g.N;
     const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (t >= per) return;
-    // splits added in order; 8 loads issued before their adds (many splits of a small C are
-    // otherwise one memory latency each)
-    float acc = P[t];
-    uint32_t s = 1;
-    for (; s + 8 <= nsplit; s += 8) {
+    // splits added in order, 8 loads issued before their adds (a split's partial is otherwise one
+    // memory latency each); past the last split the loads repeat it and are not added
+    float acc = 0.f;
+    for (uint32_t s = 0; s < nsplit; s += 8) {
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = P[(uint64_t)(s + j) * per + t];
+        for (int j = 0; j < 8; j++) v[j] = P[(uint64_t)min(s + j, nsplit - 1) * per + t];
+        if (s == 0) acc = v[0];
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc += v[j];
+        for (int j = 0; j < 8; j++)
+            if ((s > 0 || j > 0) && s + j < nsplit) acc += v[j];
     }
-    for (; s < nsplit; s++) acc += P[(uint64_t)s * per + t];
     const uint32_t tt = (uint32_t)t;                     // the launcher keeps per < 2^32
     uint32_t q = fn.div(tt);
     const uint32_t n = tt - q * g.N;
@@ -397,6 +397,215 @@ int launch_skinny(const GemmArgs& g, void* C, const void* A, const void* Bt, hip
     return MX_OK;
 }
 
+// ------------------------------------------------------------------ skinny products, B N-major
+// C[M <= 16, N] = A[M, K] . B[K, N] with B N-major (Bt's N stride 1: dot()'s B as stored, with no
+// transposed copy).  A block owns one 128-byte line of each K row -- NC columns, 64 of a 16-bit
+// type or 32 fp32 -- over a range of K: blocks of 16 columns, reading 32- or 64-byte pieces of
+// each row, stream at well under half the rate of whole lines (16-bit 4096 x 4096 read by 256
+// blocks: 16 us against 7 us).  Few column groups cannot fill the CUs, so K is split over nsplit
+// blocks as well, each writing fp32 partials [split][batch][M][N] that splitk_sum_kernel adds in
+// order (nsplit 1: C directly).  A block's W waves take consecutive K ranges and add their
+// results in wave order.
+//
+// Per wave, a chunk of KC = 64 K rows x 128 bytes is staged in LDS (8 loads of 8 rows per lane).
+// Fragments: 16-bit through two transposing LDS reads per 16-column tile (ds_read_b64_tr_b16:
+// within a 16-lane group, lanes 4e .. 4e + 3 address K row e of a 4 x 16 block, 8 bytes each, and
+// lane j receives column j); fp32 through four 4-byte reads.
+template <int DT> struct SkinnyNN {
+    using S = typename MmaTraits<DT>::S;
+    static constexpr uint32_t CE = 16 / sizeof(S);       // elements per 16-byte piece
+    static constexpr uint32_t NC = 128 / sizeof(S);      // columns per block
+    static constexpr uint32_t NT = NC / 16;              // 16-column MFMA tiles
+    static constexpr uint32_t KS = 4 * CE;               // K per MFMA step
+    static constexpr uint32_t KC = 64;                   // K rows per chunk
+    static constexpr int W = 8;                          // waves per block
+};
+
+// Blocks the split aims for (column groups x batches x splits).
+constexpr uint64_t kSkinnyNNBlocks = 256;
+
+// Byte c of staged K row r.  16-bit: a half-wave's transposing read takes one 32-byte column
+// segment of K rows b .. b + 3 and b + 8 .. b + 11 (b a multiple of 4); segment c / 32 of row r
+// sits at c / 32 ^ (bit 1 of r | bit 3 of r << 1), which gives those 8 rows 8 distinct 32-byte
+// bank groups.  fp32: a read takes 64 bytes of K rows r, r + 4, r + 8, r + 12; rows swap within
+// pairs on bit 2 of r (alternating row parity) and the 64-byte halves swap on bit 3, four
+// distinct 64-byte bank quarters.
+template <int DT>
+__device__ __forceinline__ uint32_t skinny_nn_off(uint32_t r, uint32_t c) {
+    if constexpr (DT == MX_FLOAT32)
+        return (r ^ ((r >> 2) & 1)) * 128 + (c ^ (((r >> 3) & 1) << 6));
+    else
+        return r * 128 + (c ^ ((((r >> 1) & 1) | ((r >> 2) & 2)) << 5));
+}
+
+// The N-major skinny path: at most 16 rows of A (unit K stride), B N-major, 16-byte pieces.
+template <int DT>
+bool skinny_nn_ok(const GemmArgs& g, const void* A, const void* Bt) {
+    constexpr uint32_t CE = SkinnyNN<DT>::CE;
+    if (g.M > 16 || g.ka != 1 || g.ldb != 1 || g.K % CE || g.lda % CE || g.kb % CE || g.N % CE) return false;
+    if ((uintptr_t)A % 16 || (uintptr_t)Bt % 16 || g.batches > 65535) return false;
+    for (int d = 0; d < g.bd.n; d++)
+        if (g.bd.sA[d] % CE || g.bd.sB[d] % CE) return false;
+    return true;
+}
+
+// K splits: enough for kSkinnyNNBlocks blocks, at most one per chunk of every wave.
+template <int DT>
+uint32_t skinny_nn_splits(const GemmArgs& g) {
+    using P = SkinnyNN<DT>;
+    const uint64_t blocks = (uint64_t)((g.N + P::NC - 1) / P::NC) * g.batches;
+    if (blocks >= kSkinnyNNBlocks) return 1;
+    uint64_t want = (kSkinnyNNBlocks + blocks - 1) / blocks;
+    const uint64_t most = g.K / (P::W * P::KC);
+    if (want > most) want = most;
+    return want < 1 ? 1 : (uint32_t)want;
+}
+
+// kw: K elements per wave (a multiple of one step); wave w of split sp takes K from
+// (sp W + w) kw.  SPLIT: Cv is the fp32 partials, else C.
+template <int DT, bool SPLIT>
+__global__ __launch_bounds__(64 * SkinnyNN<DT>::W) void gemm_skinny_nn_kernel(
+    void* __restrict__ Cv, const typename MmaTraits<DT>::S* __restrict__ A,
+    const typename MmaTraits<DT>::S* __restrict__ Bt, GemmArgs g, uint32_t ncg, uint32_t kw) {
+    using P = SkinnyNN<DT>;
+    using S = typename P::S;
+    using V = typename SkinnyFrag<DT>::V;
+    constexpr uint32_t CE = P::CE, NC = P::NC, NT = P::NT, KS = P::KS, KC = P::KC;
+    constexpr uint32_t SPC = KC / KS;              // MFMA steps per chunk
+    constexpr int W = P::W;
+    __shared__ __align__(16) char stage[W][KC * 128];
+    __shared__ f4v part[W - 1][NT][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t i = lane & 15, grp = lane >> 4;
+    const uint32_t cg = blockIdx.x % ncg, sp = blockIdx.x / ncg;
+    const uint32_t n0 = cg * NC;
+    uint32_t b = blockIdx.y;
+    uint64_t offA = 0, offB = 0, offC = 0;
+    for (int d = g.bd.n - 1; d >= 0; --d) {
+        const uint32_t q = g.bd.shape[d].div(b);
+        const uint32_t idx = b - q * g.bd.shape[d].d;
+        b = q;
+        offA += (uint64_t)idx * g.bd.sA[d];
+        offB += (uint64_t)idx * g.bd.sB[d];
+        offC += (uint64_t)idx * g.bd.sC[d];
+    }
+    const uint32_t kbeg = (uint32_t)min((uint64_t)g.K, ((uint64_t)sp * W + wave) * kw);
+    const uint32_t kend = min(g.K, kbeg + kw);
+    const uint32_t lr = lane >> 3, lp = lane & 7;      // K row within a load instruction, 16-byte piece
+    uint32_t pc = n0 + lp * CE;
+    if (pc >= g.N) pc = n0;                            // pieces past N re-read the group's first (never stored)
+    const S* bcol = Bt + offB + pc;
+    const S* arow = A + offA + (uint64_t)min(i, g.M - 1) * g.lda;
+    char* stb = stage[wave];
+    const V zero = {};
+    V R[8], fa[SPC];
+    f4v acc[NT];
+#pragma unroll
+    for (int t = 0; t < (int)NT; t++) acc[t] = f4v{0.f, 0.f, 0.f, 0.f};
+    // Every load is unconditional: a K row at or beyond kend is read from K row kbeg instead (in
+    // bounds) and replaced by zero where it is used.
+    auto load_chunk = [&](uint32_t kc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t k = kc + 8 * j + lr;
+            R[j] = ld_stream(reinterpret_cast<const V*>(bcol + (uint64_t)(k < kend ? k : kbeg) * g.kb));
+        }
+    };
+    auto load_a = [&](uint32_t kc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < (int)SPC; s++) {
+            const uint32_t k = kc + s * KS + grp * CE;
+            fa[s] = *reinterpret_cast<const V*>(arow + (k < kend ? k : kbeg));
+        }
+    };
+    auto stage_b = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) *reinterpret_cast<V*>(stb + skinny_nn_off<DT>(8 * j + lr, lp * 16)) = R[j];
+    };
+    // lane (i, grp)'s fragment of step s, tile t: column n0 + 16 t + i, K rows s KS + grp CE .. + CE - 1
+    auto read_b = [&](uint32_t s, uint32_t t) __attribute__((always_inline)) -> V {
+        if constexpr (DT == MX_FLOAT32) {
+            V v;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                v[j] = *reinterpret_cast<const float*>(stb + skinny_nn_off<DT>(s * KS + grp * CE + j, t * 64 + i * 4));
+            return v;
+        } else {
+            const uint32_t r = s * KS + grp * CE + (i >> 2), c = t * 32 + (lane & 3) * 8;
+            const tile::s4v lo = tile::ds_read_tr16(stb + skinny_nn_off<DT>(r, c));
+            const tile::s4v hi = tile::ds_read_tr16(stb + skinny_nn_off<DT>(r + 4, c));
+            const auto v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            V out;
+            __builtin_memcpy(&out, &v, 16);
+            return out;
+        }
+    };
+    auto compute = [&](uint32_t kc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < (int)SPC; s++) {
+            const bool ok = kc + s * KS + grp * CE < kend;
+            const V a = ok ? fa[s] : zero;
+#pragma unroll
+            for (int t = 0; t < (int)NT; t++) {
+                const V fb = read_b(s, t);
+                acc[t] = skinny_mma<DT>(ok ? fb : zero, a, acc[t]);
+            }
+        }
+    };
+    // per chunk: stage its B rows and load its A fragments, the next chunk's B loads, the MFMAs.
+    // Staging overwrites LDS this wave read for the last chunk (a wave's LDS accesses are in order).
+    const uint32_t nch = kend > kbeg ? (kend - kbeg + KC - 1) / KC : 0;
+    if (nch > 0) load_chunk(kbeg);
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint32_t kc = kbeg + c * KC;
+        stage_b();
+        load_a(kc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (c + 1 < nch) load_chunk(kc + KC);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(kc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int t = 0; t < (int)NT; t++) part[wave - 1][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < W - 1; w++) {
+#pragma unroll
+        for (int t = 0; t < (int)NT; t++) acc[t] += part[w][t][lane];
+    }
+    if (i >= g.M) return;
+    // lane (i, grp) holds C[i][n0 + 16 t + 4 grp + r] in acc[t][r]; N is a multiple of 4
+    if constexpr (SPLIT) {
+        const uint64_t per = (uint64_t)g.batches * g.M * g.N;
+        float* prow = reinterpret_cast<float*>(Cv) + sp * per + ((uint64_t)blockIdx.y * g.M + i) * g.N;
+#pragma unroll
+        for (int t = 0; t < (int)NT; t++) {
+            const uint32_t n = n0 + 16 * t + 4 * grp;
+            if (n < g.N) *reinterpret_cast<f4v*>(prow + n) = acc[t];
+        }
+    } else {
+        S* crow = reinterpret_cast<S*>(Cv) + offC + (uint64_t)i * g.ldc;
+#pragma unroll
+        for (int t = 0; t < (int)NT; t++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t n = n0 + 16 * t + 4 * grp + r;
+                if (n >= g.N) continue;
+                S o;
+                if constexpr (DT == MX_FLOAT32) o = acc[t][r];
+                else if constexpr (DT == MX_FLOAT16) o = float_to_half_bits(acc[t][r]);
+                else o = float_to_bf16(acc[t][r]);
+                crow[(uint64_t)n * g.cn] = o;
+            }
+        }
+    }
+}
+
 // Split-K when the output tiles leave most of the 256 CUs idle: enough K pieces (each at least
 // four 128-byte K pairs) to give about one block per CU (512 x 4096 x 1024: fp32 86-87 / f16 209
 // TFLOP/s, against 75 / 172 at two blocks per CU).  Returns 1 for no split.
@@ -421,6 +630,11 @@ size_t split_bytes(const GemmArgs& g) {
     using S = typename MmaTraits<DT>::S;
     alignas(16) static const char aligned[16] = {};
     if (skinny_ok<DT>(g, aligned, aligned)) return 0;
+    if (skinny_nn_ok<DT>(g, aligned, aligned)) {
+        const uint64_t per = (uint64_t)g.batches * g.M * g.N;
+        const uint32_t nsplit = skinny_nn_splits<DT>(g);
+        return nsplit > 1 && per < 0xffffffffull ? (size_t)nsplit * per * sizeof(float) : 0;
+    }
     const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
     uint32_t ksplit = 0;
     const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
@@ -438,6 +652,37 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
     if (skinny_ok<DT>(g, A, Bt)) {
         const int rc = launch_skinny<DT>(g, C, A, Bt, st);
         return rc || !epi ? rc : launch_bias_act<DT>(g, C, *epi, st);
+    }
+    if (skinny_nn_ok<DT>(g, A, Bt)) {
+        using P = SkinnyNN<DT>;
+        const uint64_t per = (uint64_t)g.batches * g.M * g.N;
+        uint32_t nsplit = skinny_nn_splits<DT>(g);
+        if (nsplit > 1 && (ws == nullptr || (uintptr_t)ws % 16 || per >= 0xffffffffull ||
+                           (size_t)nsplit * per * sizeof(float) > ws_bytes))
+            nsplit = 1;
+        uint32_t kw = (uint32_t)((g.K + (uint64_t)nsplit * P::W - 1) / ((uint64_t)nsplit * P::W));
+        kw = (kw + P::KS - 1) / P::KS * P::KS;
+        const uint32_t ncg = (g.N + P::NC - 1) / P::NC;
+        if ((uint64_t)ncg * nsplit > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_batched_matmul: grid too large");
+        const dim3 grid(ncg * nsplit, g.batches), block(64 * P::W);
+        if (nsplit == 1) {
+            hipLaunchKernelGGL((gemm_skinny_nn_kernel<DT, false>), grid, block, 0, st, C, (const S*)A, (const S*)Bt, g,
+                               ncg, kw);
+            MX_HIP(hipGetLastError());
+            return epi ? launch_bias_act<DT>(g, C, *epi, st) : MX_OK;
+        }
+        hipLaunchKernelGGL((gemm_skinny_nn_kernel<DT, true>), grid, block, 0, st, ws, (const S*)A, (const S*)Bt, g, ncg,
+                           kw);
+        MX_HIP(hipGetLastError());
+        const dim3 sgrid((uint32_t)((per + 255) / 256));
+        if (epi)
+            hipLaunchKernelGGL((splitk_sum_kernel<DT, true>), sgrid, dim3(256), 0, st, (S*)C, (const float*)ws, nsplit,
+                               g, FastDiv(g.N), FastDiv(g.M), *epi);
+        else
+            hipLaunchKernelGGL((splitk_sum_kernel<DT, false>), sgrid, dim3(256), 0, st, (S*)C, (const float*)ws, nsplit,
+                               g, FastDiv(g.N), FastDiv(g.M), Epi{});
+        MX_HIP(hipGetLastError());
+        return MX_OK;
     }
     const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
     uint32_t ksplit = 0;

@@ -911,23 +911,18 @@ matrix matrix::unbroadcast_shape(const size_m* target_shape, int target_dims) co
 }
 
 // A float Bt whose N axis is unit-stride with 16-byte K rows (B contiguous as [..., K, N], seen
-// through the transpose): the GEMM reads B in that layout (fp32 as 4-column rows, 16-bit types
-// through transposing LDS reads), so no packed copy is made.  fp32 products of at most 16 rows of A
-// keep the copy: the streaming kernel for them reads Bt K-major, and copy + streaming kernel beat
-// the N-major tile kernel there (config 3's A[8,1,4096] x B[4096,4096]: 38 vs 45 us), while for
-// 16-bit data the N-major tile kernel wins (15 vs about 20 us).
-static bool n_major_ok(const matrix& a, const matrix& bt) {
-    if (!is_floating(bt.type) || bt.dims < 2 || a.dims < 2) return false;
+// through the transpose): the GEMM reads B in that layout -- the tile kernel (fp32 as 4-column
+// rows, 16-bit types through transposing LDS reads) or, for at most 16 rows of A, the streaming
+// kernel's N-major form -- so no packed copy is made.
+static bool n_major_ok(const matrix& bt) {
+    if (!is_floating(bt.type) || bt.dims < 2) return false;
     const uint32_t ce = 16 / (uint32_t)dtype_size(bt.type);
     const size_m* st = bt.strides();
     const size_m* sh = bt.shape();
     if (st[bt.dims - 2] != 1 || st[bt.dims - 1] % ce || sh[bt.dims - 2] % ce || bt.offset % ce) return false;
     for (uint32_t d = 0; d + 2 < bt.dims; d++)
         if (sh[d] > 1 && st[d] % ce) return false;
-    if (bt.type != dtype::Float) return true;
-    uint64_t rows = 1;
-    for (uint32_t d = 0; d + 1 < a.dims; d++) rows *= a.shape()[d];
-    return rows > 16;
+    return true;
 }
 
 // A float A given M-major (a transposed view whose M axis is unit-stride, the vjp's g^T) that the
@@ -957,7 +952,7 @@ matrix matrix::dot(const matrix& b, bool transposeB) const {
         std::swap(axes[b.dims - 2], axes[b.dims - 1]);
         bt = b.transpose(axes);
     }
-    if (!bt.is_contiguous() && !(bt.type == type && n_major_ok(*this, bt))) bt = bt.astype(bt.type, true);
+    if (!bt.is_contiguous() && !(bt.type == type && n_major_ok(bt))) bt = bt.astype(bt.type, true);
     matrix a = is_contiguous() || m_major_ok(*this) ? *this : astype(type, true);
     if (bt.type != a.type) bt = bt.astype(a.type, true);
     uint32_t os[MX_MAX_DIMS], ost[MX_MAX_DIMS], b1s[MX_MAX_DIMS], b1t[MX_MAX_DIMS], b2s[MX_MAX_DIMS], b2t[MX_MAX_DIMS];

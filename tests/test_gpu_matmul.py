@@ -267,6 +267,60 @@ NN_TOL64 = {"FLOAT32": 1e-5, "FLOAT16": 2e-3, "BFLOAT16": 1e-2}   # vs fp64 of t
 
 @pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
 @pytest.mark.parametrize("case", [
+    ([8, 1, 4096], [4096, 4096]),        # the skinny workload with B as given ([K, N]): split K
+    ([16, 3000], [3000, 2048]),          # M = 16, K not a chunk multiple
+    ([1, 1024], [1024, 2056]),           # one row, N not a multiple of the column group
+    ([3, 5, 520], [3, 520, 2048]),       # per-batch B: blockIdx.y walks the batch
+    ([2, 2, 7, 64], [2, 1, 64, 1024]),   # two batch axes, one broadcast; K shorter than a chunk
+    ([4, 40], [40, 4096]),               # K = 40: most waves idle, K tail inside a step
+    ([8, 65536], [65536, 64]),           # one column group: K split many ways
+    ([2, 8], [8, 16384]),                # no split (enough column groups), K = one fragment
+])
+def test_skinny_n_major_b(mx, orc, dt, case):
+    """At most 16 rows of A with B handed over N-major: the streaming kernel reads whole 128-byte
+    lines of B's K rows, split over K when the column groups are few; checked against the oracle on
+    the packed Bt the reference's dot() builds and in fp64, with and without the split workspace,
+    and run to run bit for bit."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(19)
+    a_shape, b_shape = case
+    K, N = b_shape[-2], b_shape[-1]
+    a = gen(rng, code, a_shape, 1.0 / math.sqrt(K), mx)
+    b = gen(rng, code, b_shape, 1.0, mx)
+    bst = contiguous_strides(b_shape)
+    view = dict(bt_shape=b_shape[:-2] + [N, K], bt_strides=bst[:-2] + [1, N], oracle=False)
+    got, _, out = run_mm(mx, orc, code, a, b, **view)
+    bt = np.ascontiguousarray(np.swapaxes(b, -1, -2))
+    _, desc = matmul_desc(mx, list(a_shape), contiguous_strides(a_shape), list(bt.shape), contiguous_strides(bt.shape))
+    ref = orc.batched_matmul(code, desc, K, a.reshape(-1), bt.reshape(-1), int(np.prod(out)), acc=orc.ACC_F32)
+    ref64 = np.matmul(as_f32(code, a, mx).astype(np.float64), as_f32(code, b, mx).astype(np.float64)).reshape(-1)
+    got1, _, _ = run_mm(mx, orc, code, a, b, workspace=False, **view)
+    for g in (got, got1):
+        assert normwise_rel(as_f32(code, g, mx), as_f32(code, ref, mx)) <= TOL[dt]
+        assert normwise_rel(as_f32(code, g, mx), ref64) <= NN_TOL64[dt]
+    got2, _, _ = run_mm(mx, orc, code, a, b, **view)
+    assert np.array_equal(got, got2)
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("M", [16, 8, 3])
+def test_skinny_n_major_b_one_hot_exact(mx, orc, dt, M):
+    """One-hot A rows pick B rows exactly through the N-major streaming kernel: C[m, :] = B[k_m, :]
+    (its staged K rows, column placement and transposing reads)."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(20 + M)
+    K, N = 1000, 4096
+    ks = rng.integers(0, K, M)
+    b = gen(rng, code, [K, N], 1.0, mx)
+    a = np.zeros([M, K], b.dtype)
+    a[np.arange(M), ks] = np.array([1.0], np.float32).astype(np.float16) if code == mx.FLOAT16 else (
+        np.float32(1.0) if code == mx.FLOAT32 else np.uint16(0x3F80))
+    got, _, _ = run_mm(mx, orc, code, a, b, bt_shape=[N, K], bt_strides=[1, N], oracle=False)
+    assert np.array_equal(got.reshape(M, N), b[ks])
+
+
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
     ([2, 300, 200], [2, 200, 152]),      # ragged M, K tail, N a multiple of 8 but not of the tile
     ([512, 1024], [1024, 4096]),         # the MLP's first layer (split K)
     ([3, 130, 96], [3, 96, 264]),        # per-batch B
