@@ -15,7 +15,8 @@
 //   and the kernel into Wp [O, K.., Cgp], Cgp = C / groups rounded up to a 128-byte K pair with
 //   zero channels, flip applied.  Every K pair then lies inside one kernel position, so the A
 //   tile's DMA gathers whole 128-byte channel runs straight from Xp: one address per lane per
-//   DMA instruction, a zero page for taps outside the image.  Groups are the GEMM batch.
+//   DMA instruction, zeros for taps outside the image (an offset past the buffer resource's
+//   range).  Groups are the GEMM batch.
 // Everything else (integers, input dilation, 3+ spatial axes): a direct kernel, one output per
 //   thread, in the reference's loop order (fp32 results then equal the CPU's bit for bit).
 #include "mfma_tile.hpp"
@@ -25,8 +26,6 @@ namespace {
 
 using tile::GemmArgs;
 using tile::MmaTraits;
-
-__device__ __align__(16) uint32_t g_zero_page[4] = {0u, 0u, 0u, 0u};
 
 constexpr int kMaxSpatial = 6;
 
@@ -100,6 +99,12 @@ struct ConvSrc {
             kk[d] = (int32_t)k * geo.dil[d] - geo.pad[d];
             uoff += kk[d] * (int32_t)geo.xs[d];
         }
+#if __HIP_DEVICE_COMPILE__                               // (the buffer resource type is device-only)
+        // The buffer form of the LDS DMA from the batch's image: a tap off the image takes byte
+        // offset 2^31, past the resource's range, and the DMA writes zeros (the launcher keeps
+        // the image below 2 GiB).  The compiler counts this form in vmcnt only (see dma_rows).
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<S*>(Abat), 0, (int)0x80000000u, 0x00020000);
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             bool valid = true;
@@ -108,9 +113,11 @@ struct ConvSrc {
                 const int32_t s = (int32_t)((st.pos[i] >> (16 * d)) & 0xffffu) + kk[d];
                 valid = valid && (uint32_t)s < geo.idim[d];
             }
-            const S* src = Abat + (st.base[i] + uoff);
-            tile::dma16(valid ? (const void*)src : (const void*)g_zero_page, lds + (wave * NA + i) * 1024);
+            const uint32_t off = valid ? (uint32_t)(st.base[i] + uoff) * (uint32_t)sizeof(S) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (__attribute__((address_space(3))) void*)(lds + (wave * NA + i) * 1024), 16, off, 0, 0, 0);
         }
+#endif
     }
 
     __device__ __forceinline__ static uint64_t row_off(const GemmArgs& g, const Geom& geo, uint32_t row) {
@@ -430,7 +437,7 @@ Plan plan_conv(int dtype, const ConvShape& cs) {
     const uint64_t xp_elems = (uint64_t)cs.N * sp * cs.groups * p.Cgp;
     const uint64_t K = kp * p.Cgp;
     const uint64_t M = (uint64_t)cs.N * osp;
-    if (xp_elems >= (1ull << 31) || K >= (1ull << 31) || M >= (1ull << 32) || K * es * 256 >= (1ull << 32))
+    if (xp_elems * es >= (1ull << 31) || K >= (1ull << 31) || M >= (1ull << 32) || K * es * 256 >= (1ull << 32))
         return p;
     uint32_t ishape[kMaxSpatial + 2], kshape[kMaxSpatial + 2];
     ishape[0] = cs.N;
