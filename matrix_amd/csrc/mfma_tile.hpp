@@ -6,8 +6,9 @@
 // Matrix.mm:12274-12277).  float16 / bfloat16: v_mfma_f32_32x32x16_{f16,bf16}, fp32
 // accumulation, one rounding on store.  float32: v_mfma_f32_32x32x2_f32.
 //
-// Tiling: a 256-thread block computes a BM x BN tile of C (each 256 or 128) as 2 x 2 waves of
-// BM/2 x BN/2 (BM/64 x BN/64 MFMA tiles of 32 x 32 per wave, fp32 accumulators in AGPRs).  A K step
+// Tiling: a block computes a BM x BN tile of C (each 256 or 128) as 2 x WN waves of BM/2 x BN/WN
+// (BM/64 x BN/(32 WN) MFMA tiles of 32 x 32 per wave, fp32 accumulators): WN = 2 (256 threads),
+// or WN = 4 (512 threads, two waves per SIMD) for 16-bit 256 x 256 tiles.  A K step
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
@@ -41,7 +42,7 @@ constexpr int CPR = ROWB / 16;            // 16-byte chunks per LDS row
 constexpr int STEP_CHUNKS = STEPB / 16;
 constexpr int NTHREADS = 256;
 constexpr int NUM_XCD = 8;
-template <int ROWS> constexpr int kDma = ROWS * ROWB / 1024 / 4;   // 1 KB DMAs per wave per slot
+template <int ROWS, int NW = 4> constexpr int kDma = ROWS * ROWB / 1024 / NW;   // 1 KB DMAs per wave per slot
 
 template <int DT> struct MmaTraits;
 template <> struct MmaTraits<MX_FLOAT16> { using S = uint16_t; };
@@ -88,16 +89,16 @@ __device__ __forceinline__ void tile_of(uint32_t id, uint32_t nblocks, uint32_t 
 // through registers, element loads, zero past K (zeros keep the tail exact).  This thread's
 // chunk q = tid + 256 i is row q / 4, logical chunk q % 4.  Rows past the operand's end re-read
 // its last row (their products land only in C rows / columns that are never stored).
-template <int ROWS> constexpr int kTailChunks = ROWS * STEP_CHUNKS / NTHREADS;
+template <int ROWS, int NT = NTHREADS> constexpr int kTailChunks = ROWS * STEP_CHUNKS / NT;
 
-template <typename S, int ROWS>
-__device__ __forceinline__ void load_tile_guarded(uint4 (&r)[kTailChunks<ROWS>], const S* __restrict__ base,
+template <typename S, int ROWS, int NT = NTHREADS>
+__device__ __forceinline__ void load_tile_guarded(uint4 (&r)[(kTailChunks<ROWS, NT>)], const S* __restrict__ base,
                                                   uint32_t rows_valid, uint32_t ld, uint32_t kstride, uint32_t k0,
                                                   uint32_t K) {
     constexpr int CE = 16 / sizeof(S);
 #pragma unroll
-    for (int i = 0; i < kTailChunks<ROWS>; i++) {
-        const int q = threadIdx.x + NTHREADS * i;
+    for (int i = 0; i < kTailChunks<ROWS, NT>; i++) {
+        const int q = threadIdx.x + NT * i;
         const uint32_t row = min((uint32_t)(q / STEP_CHUNKS), rows_valid - 1);
         const uint32_t k = k0 + (q % STEP_CHUNKS) * CE;
         S tmp[CE];
@@ -108,11 +109,11 @@ __device__ __forceinline__ void load_tile_guarded(uint4 (&r)[kTailChunks<ROWS>],
     }
 }
 
-template <int ROWS>
-__device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[kTailChunks<ROWS>]) {
+template <int ROWS, int NT = NTHREADS>
+__device__ __forceinline__ void store_tile(char* lds, const uint4 (&r)[(kTailChunks<ROWS, NT>)]) {
 #pragma unroll
-    for (int i = 0; i < kTailChunks<ROWS>; i++) {
-        const int q = threadIdx.x + NTHREADS * i;
+    for (int i = 0; i < kTailChunks<ROWS, NT>; i++) {
+        const int q = threadIdx.x + NT * i;
         const int row = q / STEP_CHUNKS, c = q % STEP_CHUNKS;
         *reinterpret_cast<uint4*>(lds + row * ROWB + swz(row, c) * 16) = r[i];
     }
@@ -499,14 +500,15 @@ __device__ __forceinline__ DmaOffsets<N> dma_offsets_nn16(uint32_t cols_valid, u
 // One K step (32 rows) of the 16-bit N-major B tile through registers, element loads, zero past K
 // and past N, into rows 0 .. 31 of the slot.  Thread chunk q = tid + 256 j is K row q / (BN / 8),
 // logical chunk q % (BN / 8).
-template <int BN> constexpr int kTailChunksNN16 = 32 * (BN / 8) / NTHREADS;
+template <int BN, int NT = NTHREADS> constexpr int kTailChunksNN16 = 32 * (BN / 8) / NT;
 
-template <int BN>
-__device__ __forceinline__ void load_tile_guarded_nn16(uint4 (&r)[kTailChunksNN16<BN>], const uint16_t* __restrict__ base,
-                                                       uint32_t cols_valid, uint32_t ldk, uint32_t k0, uint32_t K) {
+template <int BN, int NT = NTHREADS>
+__device__ __forceinline__ void load_tile_guarded_nn16(uint4 (&r)[(kTailChunksNN16<BN, NT>)],
+                                                       const uint16_t* __restrict__ base, uint32_t cols_valid,
+                                                       uint32_t ldk, uint32_t k0, uint32_t K) {
 #pragma unroll
-    for (int j = 0; j < kTailChunksNN16<BN>; j++) {
-        const int q = threadIdx.x + NTHREADS * j;
+    for (int j = 0; j < kTailChunksNN16<BN, NT>; j++) {
+        const int q = threadIdx.x + NT * j;
         const uint32_t k = k0 + (uint32_t)(q / (BN / 8));
         const uint32_t c = (uint32_t)(q % (BN / 8)) * 8;
         uint16_t tmp[8];
@@ -516,11 +518,11 @@ __device__ __forceinline__ void load_tile_guarded_nn16(uint4 (&r)[kTailChunksNN1
     }
 }
 
-template <int BN>
-__device__ __forceinline__ void store_tile_nn16(char* lds, const uint4 (&r)[kTailChunksNN16<BN>]) {
+template <int BN, int NT = NTHREADS>
+__device__ __forceinline__ void store_tile_nn16(char* lds, const uint4 (&r)[(kTailChunksNN16<BN, NT>)]) {
 #pragma unroll
-    for (int j = 0; j < kTailChunksNN16<BN>; j++) {
-        const int q = threadIdx.x + NTHREADS * j;
+    for (int j = 0; j < kTailChunksNN16<BN, NT>; j++) {
+        const int q = threadIdx.x + NT * j;
         const int row = q / (BN / 8), c = q % (BN / 8);
         *reinterpret_cast<uint4*>(lds + row * (BN * 2) + swz_nn16(row, c) * 16) = r[j];
     }
@@ -537,8 +539,7 @@ __device__ __forceinline__ void wait_vmem() {
 // Instruction order within a K step, so the LDS and the memory pipeline work under the matrix
 // core instead of before it (sched_group_barrier masks: 0x008 MFMA, 0x100 LDS read, 0x020
 // vector-memory read).  A slot is one MFMA for 16-bit types and four for fp32; a step has
-// 2 TM WNT slots, 2 (TM + WNT) fragment reads, and a pair kDma<BM> + kDma<BN> instructions per
-// wave.  The fragment reads go out early in their window so that they have returned (LDS
+// 2 TM WNT slots, 2 (TM + WNT) fragment reads, and a pair's ND DMA instructions per wave.  The fragment reads go out early in their window so that they have returned (LDS
 // latency is several MFMAs) before the next step's first MFMA needs them.
 template <int DT> constexpr int kMfmaPerSlot = DT == MX_FLOAT32 ? 4 : 1;
 
@@ -561,9 +562,9 @@ __device__ __forceinline__ void interleave_even() {
 
 // Second step of a pair, after its barrier (TM WNT slots left): the next step's fragment reads
 // over the first half of the slots, the DMA of the pair two ahead over all of them.
-template <int DT, int TM, int WNT, int BM, int BN, int NR>
+template <int DT, int TM, int WNT, int ND, int NR>
 __device__ __forceinline__ void interleave_odd() {
-    constexpr int MF = kMfmaPerSlot<DT>, H = TM * WNT, ND = kDma<BM> + kDma<BN>;
+    constexpr int MF = kMfmaPerSlot<DT>, H = TM * WNT;
     constexpr int RPS = NR / (H / 2);                          // reads per slot, first half
     constexpr int D1 = (ND + H - 1) / H;                       // DMAs per slot, first half
     constexpr int D2 = (ND - D1 * (H / 2)) / (H / 2);          // DMAs per slot, second half
@@ -606,11 +607,11 @@ __device__ __forceinline__ void ring_barrier() {
 // row bytes.  The quarter is written to LDS whole (16-byte chunk c of row r at
 // c ^ (r mod chunks per row)), then read back and stored row-major.  Otherwise an interior tile
 // stores 4 columns per instruction from the fragments, and other tiles one element at a time.
-template <int DT, int BM, int BN, bool SPLIT, class Src, bool STAGE, typename CT, bool RT = false>
-__device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN / 64], const GemmArgs& g,
+template <int DT, int BM, int BN, int WN, bool SPLIT, class Src, bool STAGE, typename CT, bool RT = false>
+__device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN / (32 * WN)], const GemmArgs& g,
                                         const typename Src::Geom& geo, uint32_t m0, uint32_t n0, int wm, int wn, int lane,
                                         bool vec_store, char* stage) {
-    constexpr int TM = BM / 64, WNT = BN / 64;
+    constexpr int TM = BM / 64, WNT = BN / (32 * WN);
     const int h = lane >> 5, c32 = lane & 31;
     // row of accumulator tile i within the wave's range (RT: fp32 M-major A, Frags32T)
     auto rin = [&](int i) { return RT ? TM * c32 + i : i * 32 + c32; };
@@ -709,25 +710,27 @@ __device__ __forceinline__ void store_c(CT* Cbat, const f16v (&acc)[BM / 64][BN 
 //   uint64_t row_off(g, geo, row)         element offset of C row `row` (batch offset apart)
 //   bool row_vec_ok<S>(g, geo)            every row offset is a multiple of 16 bytes
 // (NA = DMA instructions per wave for the A slot.)  Tiles are BM x BN with BM, BN in {128, 256}:
-// 2 x 2 waves of (BM / 2) x (BN / 2).  A 128 x 128 tile needs 64 KB of LDS, so two blocks share
+// 2 x WN waves of (BM / 2) x (BN / WN).  A 128 x 128 tile needs 64 KB of LDS, so two blocks share
 // a CU.
 // SPLIT: the K range is cut into g.ksplit-element pieces, one per block along the outermost
 // block-batch index; the block writes its fp32 partial tile to Cv as [split][batch][M][N]
 // (g.ldc = N, g.cn = 1), and a second kernel sums the splits in order.
 // BNN: Bt is N-major (B as [K, N]: g.ldb == 1, g.kb is B's row stride); fp32 reads it as FragsNN
 // describes, 16-bit types through transposing LDS reads (read_frags_nn16).
-template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src, bool BNN = false, bool AMN = false>
-__global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ Cv,
+template <int DT, int BM, int BN, bool VEC, bool SPLIT, class Src, bool BNN = false, bool AMN = false, int WN = 2>
+__global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ Cv,
                                                              const typename MmaTraits<DT>::S* __restrict__ A,
                                                              const typename MmaTraits<DT>::S* __restrict__ Bt,
                                                              GemmArgs g, typename Src::Geom geo) {
     using S = typename MmaTraits<DT>::S;
     using CT = std::conditional_t<SPLIT, float, S>;    // element type written to Cv
+    static_assert(WN == 2 || (WN == 4 && DT != MX_FLOAT32), "eight waves: 16-bit types only");
+    constexpr int NW = 2 * WN, NT = 64 * NW;           // waves (2 along M, WN along N), threads
     constexpr int TM = BM / 64;                        // A tiles of 32 rows per wave
-    constexpr int WNT = BN / 64;                       // Bt tiles of 32 rows per wave
+    constexpr int WNT = BN / (32 * WN);                // Bt tiles of 32 rows per wave
     constexpr int KSTEP = STEPB / sizeof(S);           // elements of K per step
     constexpr int SLOT_A = BM * ROWB, SLOT_B = BN * ROWB;
-    constexpr int DMA_A = kDma<BM>, DMA_B = kDma<BN>;
+    constexpr int DMA_A = kDma<BM, NW>, DMA_B = kDma<BN, NW>;
     // two pair slots per operand, each its own array so the compiler tells the DMA into one
     // slot from the fragment reads of the other
     __shared__ __align__(16) char la0[SLOT_A], la1[SLOT_A];
@@ -774,7 +777,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
     // the wave index is wave-uniform: keeping it in a scalar register keeps every LDS slot
     // address derived from it (the DMA destinations) scalar too
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
 
     constexpr bool NN32 = BNN && DT == MX_FLOAT32;      // fp32 N-major B (FragsNN)
     constexpr bool NN16 = BNN && DT != MX_FLOAT32;      // 16-bit N-major B (transposing reads)
@@ -866,7 +869,7 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
             read_step(I0{}, f0, slot_a(SN{}), slot_b(SN{}));
         }
         mma(IH{}, ITM{}, f1);
-        if constexpr (DT != MX_FLOAT32) interleave_odd<DT, TM, WNT, BM, BN, NREADS>();
+        if constexpr (DT != MX_FLOAT32) interleave_odd<DT, TM, WNT, PER_PAIR, NREADS>();
         __builtin_amdgcn_sched_barrier(0);
     };
     // the last pairs: no DMA past the end, no barrier after the last
@@ -917,26 +920,26 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
                 load_tile_guarded_nn<BM>(ra, reinterpret_cast<const float*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
                 store_tile_nn<BM>(la0, ra);
             } else if constexpr (AMN) {
-                uint4 ra[kTailChunksNN16<BM>];
-                load_tile_guarded_nn16<BM>(ra, reinterpret_cast<const uint16_t*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
-                store_tile_nn16<BM>(la0, ra);
+                uint4 ra[kTailChunksNN16<BM, NT>];
+                load_tile_guarded_nn16<BM, NT>(ra, reinterpret_cast<const uint16_t*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
+                store_tile_nn16<BM, NT>(la0, ra);
             } else {
-                uint4 ra[kTailChunks<BM>];
-                load_tile_guarded<S, BM>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
-                store_tile<BM>(la0, ra);
+                uint4 ra[kTailChunks<BM, NT>];
+                load_tile_guarded<S, BM, NT>(ra, Ablk, rows_a, g.lda, g.ka, kt * KSTEP, Klen);
+                store_tile<BM, NT>(la0, ra);
             }
             if constexpr (NN32) {
                 f4v rb[kTailChunksNN<BN>];
                 load_tile_guarded_nn<BN>(rb, reinterpret_cast<const float*>(Bblk), rows_b, g.kb, kt * KSTEP, Klen);
                 store_tile_nn<BN>(lb0, rb);
             } else if constexpr (NN16) {
-                uint4 rb[kTailChunksNN16<BN>];
-                load_tile_guarded_nn16<BN>(rb, Bblk, rows_b, g.kb, kt * KSTEP, Klen);
-                store_tile_nn16<BN>(lb0, rb);
+                uint4 rb[kTailChunksNN16<BN, NT>];
+                load_tile_guarded_nn16<BN, NT>(rb, Bblk, rows_b, g.kb, kt * KSTEP, Klen);
+                store_tile_nn16<BN, NT>(lb0, rb);
             } else {
-                uint4 rb[kTailChunks<BN>];
-                load_tile_guarded<S, BN>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
-                store_tile<BN>(lb0, rb);
+                uint4 rb[kTailChunks<BN, NT>];
+                load_tile_guarded<S, BN, NT>(rb, Bblk, rows_b, g.ldb, g.kb, kt * KSTEP, Klen);
+                store_tile<BN, NT>(lb0, rb);
             }
             __syncthreads();
             read_step(I0{}, f0, la0, lb0);
@@ -978,11 +981,13 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
         }
         return;
     }
-    // the epilogue's LDS stage: this wave's quarter of C in one of the four slot arrays (free now:
-    // every wave has passed the barrier after its last fragment reads)
-    constexpr bool STAGE = (BM / 2) * (BN / 2) * (int)sizeof(CT) <= (SLOT_A < SLOT_B ? SLOT_A : SLOT_B);
-    char* stage = wave == 0 ? la0 : wave == 1 ? la1 : wave == 2 ? lb0 : lb1;
-    store_c<DT, BM, BN, SPLIT, Src, STAGE, CT, T32>(Cbat, acc, g, geo, m0, n0, wm, wn, lane, vec_store, stage);
+    // the epilogue's LDS stage: this wave's part of C (NW / 4 waves per slot array) in one of the
+    // four slot arrays (free now: every wave has passed the barrier after its last fragment reads)
+    constexpr int QB = (BM / 2) * (BN / WN) * (int)sizeof(CT), WPS = NW / 4;
+    constexpr bool STAGE = QB * WPS <= (SLOT_A < SLOT_B ? SLOT_A : SLOT_B);
+    const int sw = wave / WPS;
+    char* stage = (sw == 0 ? la0 : sw == 1 ? la1 : sw == 2 ? lb0 : lb1) + (wave % WPS) * QB;
+    store_c<DT, BM, BN, WN, SPLIT, Src, STAGE, CT, T32>(Cbat, acc, g, geo, m0, n0, wm, wn, lane, vec_store, stage);
 }
 
 // Tile shape for a problem: 256 x 256 tiles while they give at least one block per CU (256), 256 x
@@ -991,6 +996,12 @@ __global__ __launch_bounds__(NTHREADS) void mfma_tile_kernel(void* __restrict__ 
 // 101-107 / 510; the f16 3 x 3 convolution's 392 tiles of 256 x 128 ran 34.7 us against 32.2 us
 // on 128 x 128.
 struct TileShape { int bm, bn; };
+
+// 16-bit 256 x 256 tiles run eight waves (2 x 4, 128 x 64 each): two waves per SIMD, so one
+// wave's MFMAs cover the other's waits (config 3's f16 product: 1001-1008 -> 1026-1034 TFLOP/s in
+// one process, B read N-major 1043-1047 -> 1085), against 1.5x the fragment reads of 128 x 128
+// wave tiles.
+constexpr bool kWide16 = true;
 inline TileShape choose_tile(uint64_t M, uint64_t N, uint64_t batches) {
     const int bn = N <= 128 ? 128 : 256;
     const uint64_t big = (M + 255) / 256 * ((N + bn - 1) / bn) * batches;
@@ -1004,22 +1015,27 @@ template <int DT, bool VEC, bool SPLIT, class Src, bool BNN = false, bool AMN = 
 int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C, const void* A, const void* Bt,
                        hipStream_t st, const char* who, uint32_t nsplit = 1) {
     using S = typename MmaTraits<DT>::S;
-    auto go = [&](auto bm, auto bn) -> int {
-        constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
+    auto go = [&](auto bm, auto bn, auto wn) -> int {
+        constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value, WN = decltype(wn)::value;
         g.tiles_m = (g.M + BM - 1) / BM;
         g.tiles_n = (g.N + BN - 1) / BN;
         const uint64_t blocks = (uint64_t)g.tiles_m * g.tiles_n * g.batches * nsplit;
         if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, std::string(who) + ": grid too large");
-        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src, BNN, AMN>), dim3((uint32_t)blocks),
-                           dim3(NTHREADS), 0, st, C, (const S*)A, (const S*)Bt, g, geo);
+        hipLaunchKernelGGL((mfma_tile_kernel<DT, BM, BN, VEC, SPLIT, Src, BNN, AMN, WN>), dim3((uint32_t)blocks),
+                           dim3(128 * WN), 0, st, C, (const S*)A, (const S*)Bt, g, geo);
         MX_HIP(hipGetLastError());
         return MX_OK;
     };
+    using I2 = std::integral_constant<int, 2>;
     using I128 = std::integral_constant<int, 128>;
     using I256 = std::integral_constant<int, 256>;
-    if (ts.bm == 256 && ts.bn == 256) return go(I256{}, I256{});
-    if (ts.bm == 256) return go(I256{}, I128{});
-    return go(I128{}, I128{});
+    if (ts.bm == 256 && ts.bn == 256) {
+        if constexpr (DT != MX_FLOAT32)
+            if (kWide16) return go(I256{}, I256{}, std::integral_constant<int, 4>{});
+        return go(I256{}, I256{}, I2{});
+    }
+    if (ts.bm == 256) return go(I256{}, I128{}, I2{});
+    return go(I128{}, I128{}, I2{});
 }
 
 // A strided matrix operand (batched MatMul).
