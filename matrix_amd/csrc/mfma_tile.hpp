@@ -8,7 +8,7 @@
 //
 // Tiling: a block computes a BM x BN tile of C (each 256 or 128) as 2 x WN waves of BM/2 x BN/WN
 // (BM/64 x BN/(32 WN) MFMA tiles of 32 x 32 per wave, fp32 accumulators): WN = 2 (256 threads),
-// or WN = 4 (512 threads, two waves per SIMD) for 16-bit 256 x 256 tiles.  A K step
+// or WN = 4 (512 threads) for 16-bit 256 x 256 and 128 x 128 tiles.  A K step
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
@@ -997,10 +997,11 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
 // on 128 x 128.
 struct TileShape { int bm, bn; };
 
-// 16-bit 256 x 256 tiles run eight waves (2 x 4, 128 x 64 each): two waves per SIMD, so one
-// wave's MFMAs cover the other's waits (config 3's f16 product: 1001-1008 -> 1026-1034 TFLOP/s in
-// one process, B read N-major 1043-1047 -> 1085), against 1.5x the fragment reads of 128 x 128
-// wave tiles.
+// 16-bit 256 x 256 and 128 x 128 tiles run eight waves (2 x 4: 128 x 64 / 64 x 32 each), twice
+// the waves per SIMD, so one wave's MFMAs cover another's waits, against 1.5x the fragment reads.
+// Config 3's f16 product: 1001-1008 -> 1026-1034 TFLOP/s in one process, B read N-major
+// 1043-1047 -> 1085; config 4's f16 3x3 convolution 26.5 -> 25.5 us, 1x1 stride 2 12.8 -> 12.2 us.
+// (256 x 256 convolution tiles keep four: the gather's per-lane state would spill.)
 constexpr bool kWide16 = true;
 inline TileShape choose_tile(uint64_t M, uint64_t N, uint64_t batches) {
     const int bn = N <= 128 ? 128 : 256;
@@ -1030,11 +1031,13 @@ int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C
     using I128 = std::integral_constant<int, 128>;
     using I256 = std::integral_constant<int, 256>;
     if (ts.bm == 256 && ts.bn == 256) {
-        if constexpr (DT != MX_FLOAT32)
+        if constexpr (DT != MX_FLOAT32 && Src::kStrided)     // (the gather's state would spill)
             if (kWide16) return go(I256{}, I256{}, std::integral_constant<int, 4>{});
         return go(I256{}, I256{}, I2{});
     }
     if (ts.bm == 256) return go(I256{}, I128{}, I2{});
+    if constexpr (DT != MX_FLOAT32)
+        if (kWide16) return go(I128{}, I128{}, std::integral_constant<int, 4>{});
     return go(I128{}, I128{}, I2{});
 }
 
