@@ -12,7 +12,7 @@
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
-// global_load_lds_dwordx4) fill the slot of pair p + 2 while pair p + 1 is consumed; fragments
+// buffer_load_dwordx4 ... lds) fill the slot of pair p + 2 while pair p + 1 is consumed; fragments
 // are double-buffered in registers, and the workgroup meets one barrier per pair.  Each slot is
 // its own __shared__ array, so the compiler can tell the DMA into one slot from the reads of the
 // other and adds no waits of its own.  LDS rows are 8 chunks of 16 bytes, swizzled so that one
@@ -21,7 +21,7 @@
 //
 // Where the A rows come from is a policy (Src): a strided matrix (GEMM) or an on-the-fly
 // im2col gather from a channels-last image (implicit-GEMM convolution), whose out-of-image
-// taps read a zero page.  The same policy maps a C row to its output offset.
+// taps read zeros.  The same policy maps a C row to its output offset.
 #pragma once
 #include "common.hpp"
 
