@@ -606,6 +606,17 @@ __global__ __launch_bounds__(64 * SkinnyNN<DT>::W) void gemm_skinny_nn_kernel(
     }
 }
 
+// The tile shape of a product: tile::choose_tile's, except that an fp32 A given M-major (unit M
+// stride, the vjp's g^T) takes 128 x 128 tiles where that would choose 256 x 256, whose M-major
+// fragments spill 48-64 registers (config 5's dW2 = h1^T g2, 4096 x 4096 x 512: the step 0.634-0.643
+// -> 0.619-0.626 ms; 256 x 128 tiles no faster).
+template <int DT>
+tile::TileShape tile_for(const GemmArgs& g) {
+    tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
+    if (DT == MX_FLOAT32 && g.lda == 1 && g.ka != 1 && ts.bm == 256 && ts.bn == 256) ts = tile::TileShape{128, 128};
+    return ts;
+}
+
 // Split-K when the output tiles leave most of the 256 CUs idle: enough K pieces (each at least
 // four 128-byte K pairs) to give about one block per CU (512 x 4096 x 1024: fp32 86-87 / f16 209
 // TFLOP/s, against 75 / 172 at two blocks per CU).  Returns 1 for no split.
@@ -635,7 +646,7 @@ size_t split_bytes(const GemmArgs& g) {
         const uint32_t nsplit = skinny_nn_splits<DT>(g);
         return nsplit > 1 && per < 0xffffffffull ? (size_t)nsplit * per * sizeof(float) : 0;
     }
-    const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
+    const tile::TileShape ts = tile_for<DT>(g);
     uint32_t ksplit = 0;
     const uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
     const uint64_t per = (uint64_t)g.batches * g.M * g.N;
@@ -684,7 +695,7 @@ int launch_mfma(GemmArgs& g, void* C, const void* A, const void* Bt, void* ws, s
         MX_HIP(hipGetLastError());
         return MX_OK;
     }
-    const tile::TileShape ts = tile::choose_tile(g.M, g.N, g.batches);
+    const tile::TileShape ts = tile_for<DT>(g);
     uint32_t ksplit = 0;
     uint32_t nsplit = choose_split(ts, g, tile::ROWB / sizeof(S), &ksplit);
     const uint64_t per = (uint64_t)g.batches * g.M * g.N;
