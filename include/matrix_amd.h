@@ -196,7 +196,8 @@ int mx_launch_batched_matmul(int dtype, int cdims, const uint32_t* shapeC,
 
 /* mx_launch_batched_matmul with a caller workspace, as the reference's primitives allocate
  * during COMPILE and never during EXECUTE (primitives.cpp:454-470): when the output has too few
- * tiles to fill the CUs, the K range is split over blocks, the fp32 partials go to the
+ * tiles to fill the CUs (or, for at most 16 rows of A with Bt N-major, too few 128-byte column
+ * groups), the K range is split over blocks, the fp32 partials go to the
  * workspace and a second launch sums them in split order (deterministic).  The size comes from
  * mx_matmul_workspace_bytes (0: the product never splits, workspace may be NULL); a workspace
  * smaller than that (or NULL) runs the product unsplit.  Results differ from the unsplit form
