@@ -8,7 +8,8 @@
 //
 // Tiling: a block computes a BM x BN tile of C (each 256 or 128) as 2 x WN waves of BM/2 x BN/WN
 // (BM/64 x BN/(32 WN) MFMA tiles of 32 x 32 per wave, fp32 accumulators): WN = 2 (256 threads),
-// or WN = 4 (512 threads) for 16-bit 256 x 256 and 128 x 128 tiles.  A K step
+// or WN = 4 (512 threads) for 16-bit 256 x 256 and 128 x 128 tiles and K-major fp32 128 x 128
+// ones.  A K step
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
@@ -730,7 +731,7 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
                                                              GemmArgs g, typename Src::Geom geo) {
     using S = typename MmaTraits<DT>::S;
     using CT = std::conditional_t<SPLIT, float, S>;    // element type written to Cv
-    static_assert(WN == 2 || (WN == 4 && DT != MX_FLOAT32), "eight waves: 16-bit types only");
+    static_assert(WN == 2 || (WN == 4 && (DT != MX_FLOAT32 || (!BNN && !AMN))), "eight waves: 16-bit or K-major fp32");
     constexpr int NW = 2 * WN, NT = 64 * NW;           // waves (2 along M, WN along N), threads
     constexpr int TM = BM / 64;                        // A tiles of 32 rows per wave
     constexpr int WNT = BN / (32 * WN);                // Bt tiles of 32 rows per wave
@@ -1003,8 +1004,10 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
 // on 128 x 128.
 struct TileShape { int bm, bn; };
 
-// 16-bit 256 x 256 and 128 x 128 tiles run eight waves (2 x 4: 128 x 64 / 64 x 32 each), twice
-// the waves per SIMD, so one wave's MFMAs cover another's waits, against 1.5x the fragment reads.
+// 16-bit 256 x 256 and 128 x 128 tiles, and fp32 128 x 128 tiles with both operands K-major, run
+// eight waves (2 x 4: 128 x 64 / 64 x 32 each), twice the waves per SIMD, so one wave's MFMAs cover
+// another's waits, against 1.5x the fragment reads (fp32: the 3x3 convolution 157 -> 154 us, the
+// MLP step 0.606-0.616 -> 0.601 ms).
 // Config 3's f16 product: 1001-1008 -> 1026-1034 TFLOP/s in one process, B read N-major
 // 1043-1047 -> 1085; config 4's f16 3x3 convolution 26.5 -> 25.5 us, 1x1 stride 2 12.8 -> 12.2 us.
 // (256 x 256 convolution tiles keep four: the gather's per-lane state would spill.)
@@ -1042,7 +1045,7 @@ int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C
         return go(I256{}, I256{}, I2{});
     }
     if (ts.bm == 256) return go(I256{}, I128{}, I2{});
-    if constexpr (DT != MX_FLOAT32)
+    if constexpr (DT != MX_FLOAT32 || (!BNN && !AMN))
         if (kWide16) return go(I128{}, I128{}, std::integral_constant<int, 4>{});
     return go(I128{}, I128{}, I2{});
 }
