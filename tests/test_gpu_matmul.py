@@ -90,6 +90,22 @@ def test_float_matmul_shapes(mx, orc, dt, case):
     assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("K", [200, 201])
+def test_large_tiles_ragged(mx, orc, dt, K):
+    """256 x 256 tiles (17 x 16 of them) with ragged M and N edges: K = 200 leaves a K tail after
+    the DMA'd pairs, K = 201 makes 16-bit rows misaligned so every step goes through the guarded
+    element loads (for 16-bit types with eight waves per block).  Checked in fp64 with numpy."""
+    code = getattr(mx, dt)
+    rng = np.random.default_rng(21)
+    M, N = 4100, 4000
+    a = gen(rng, code, [M, K], 1.0 / math.sqrt(K), mx)
+    bt = gen(rng, code, [N, K], 1.0, mx)
+    got, _, _ = run_mm(mx, orc, code, a, bt, oracle=False)
+    ref64 = as_f32(code, a, mx).astype(np.float64) @ as_f32(code, bt, mx).astype(np.float64).T
+    assert normwise_rel(as_f32(code, got, mx), ref64.reshape(-1)) <= NN_TOL64[dt]
+
+
 @pytest.mark.parametrize("dt", ["FLOAT32", "FLOAT16"])
 def test_main_matmul_shape_reduced_batch(mx, orc, dt):
     """A[2,2048,2048] x B[2048,2048] (B broadcast): the batched-matmul workload's shape at batch 2."""
