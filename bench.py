@@ -317,6 +317,51 @@ def matmul_graph_case(mx, dt, kind, rng):
     return launch
 
 
+def library_gemm_tflops(mx, dt, rng, reps=20):
+    """Config 3's main product folded (C[32768, 2048] = A[32768, 2048] . B[2048, 2048]) through
+    the vendor library on the same box -- rocBLAS's gemm_ex (f16 in, fp32 compute; fp32), called
+    through ctypes on the same N(0,1)/sqrt(2048) data -- as a comparison point.  None when rocBLAS
+    cannot be loaded or refuses the call."""
+    import ctypes
+    try:
+        rb = ctypes.CDLL("librocblas.so")
+    except OSError:
+        try:
+            rb = ctypes.CDLL("/opt/rocm/lib/librocblas.so")
+        except OSError:
+            return None
+    M, N, K = 32768, 2048, 2048
+    a = _normal(rng, [M, K], 1 / np.sqrt(2048), dt)
+    bt = _normal(rng, [N, K], 1 / np.sqrt(2048), dt)
+    A, B = mx.DeviceBuffer.from_numpy(a), mx.DeviceBuffer.from_numpy(bt)
+    C = mx.DeviceBuffer(M * N * a.itemsize)
+    h, stream = ctypes.c_void_p(), ctypes.c_void_p()
+    if rb.rocblas_create_handle(ctypes.byref(h)) != 0:
+        return None
+    mx.check(mx.lib.mx_hip_stream_for_thread(ctypes.byref(stream)))    # the stream _timed's events see
+    if rb.rocblas_set_stream(h, stream) != 0:
+        rb.rocblas_destroy_handle(h)
+        return None
+    f16, f32 = 150, 151                                  # rocblas_datatype_f16_r / f32_r
+    io = f16 if dt == "f16" else f32
+    one, zero = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    # row-major C = A Bt^T is column-major C^T = Bt^T(op T of the [K x N] Bt) . A([K x M])
+    args = (h, 112, 111, N, M, K, ctypes.byref(one), ctypes.c_void_p(B.ptr), io, K, ctypes.c_void_p(A.ptr), io, K,
+            ctypes.byref(zero), ctypes.c_void_p(C.ptr), io, N, ctypes.c_void_p(C.ptr), io, N, f32, 0, 0, 0)
+
+    def launch(i=0):
+        st = rb.rocblas_gemm_ex(*args)
+        if st != 0:
+            raise RuntimeError(f"rocblas_gemm_ex status {st}")
+    try:
+        ms = min(_timed(mx, launch, reps) for _ in range(2))
+    except RuntimeError:
+        return None
+    finally:
+        rb.rocblas_destroy_handle(h)
+    return round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
+
+
 def config_matmul(mx):
     """Config 3: A[16,2048,2048] x B[2048,2048] (B broadcast over the batch), f32 and f16 with
     fp32 accumulation; skinny A[8,1,4096] x B[4096,4096].  B^T is packed once (dot's copy) and
@@ -328,7 +373,9 @@ def config_matmul(mx):
         ms = _timed(mx, launch, 5 if dt == "f32" else 20)
         tf = 274_877_906_944 / (ms * 1e-3) / 1e12
         res[f"main_{dt}"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
-                             "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)}
+                             "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4),
+                             "rocblas_TFLOP/s": library_gemm_tflops(mx, dt, rng),
+                             "note": "rocblas_TFLOP/s: the vendor library on the same box, same folded product"}
         cpu_in[f"main_{dt}"] = host
         del launch
         launch, host = matmul_case(mx, dt, "skinny", rng)
