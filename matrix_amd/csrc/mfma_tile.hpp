@@ -858,6 +858,9 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
     auto pair_steady = [&](auto s, uint32_t p) {
         using SN = std::integral_constant<int, 1 - decltype(s)::value>;
         constexpr int MF = kMfmaPerSlot<DT>;
+        // a wave between barriers runs its MFMAs at raised priority, ahead of a wave on the same
+        // SIMD that is issuing its DMA and fragment reads after the barrier (f16 GEMM +2%)
+        __builtin_amdgcn_s_setprio(1);
         read_step(I1{}, f1, slot_a(s), slot_b(s));
         mma(I0{}, ITM{}, f0);
         if constexpr (DT != MX_FLOAT32) interleave_even<DT, TM, WNT, NREADS>();
@@ -865,6 +868,7 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
         mma(I0{}, IH{}, f1);
         if constexpr (DT != MX_FLOAT32) __builtin_amdgcn_sched_group_barrier(0x008, TM * WNT * MF, 0);
         __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
         wait_vmem<0>();
         ring_barrier();
         if constexpr (DT == MX_FLOAT32) {
