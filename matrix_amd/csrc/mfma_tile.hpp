@@ -8,8 +8,7 @@
 //
 // Tiling: a block computes a BM x BN tile of C (each 256 or 128) as 2 x WN waves of BM/2 x BN/WN
 // (BM/64 x BN/(32 WN) MFMA tiles of 32 x 32 per wave, fp32 accumulators): WN = 2 (256 threads),
-// or WN = 4 (512 threads) for 16-bit 256 x 256 and 128 x 128 tiles and K-major fp32 128 x 128
-// ones.  A K step
+// or WN = 4 (512 threads) for 16-bit and K-major fp32 256 x 256 and 128 x 128 tiles.  A K step
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
@@ -1008,10 +1007,11 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
 // on 128 x 128.
 struct TileShape { int bm, bn; };
 
-// 16-bit 256 x 256 and 128 x 128 tiles, and fp32 128 x 128 tiles with both operands K-major, run
-// eight waves (2 x 4: 128 x 64 / 64 x 32 each), twice the waves per SIMD, so one wave's MFMAs cover
-// another's waits, against 1.5x the fragment reads (fp32: the 3x3 convolution 157 -> 154 us, the
-// MLP step 0.606-0.616 -> 0.601 ms).
+// 16-bit tiles and fp32 tiles with both operands K-major (256 x 256 and 128 x 128) run eight waves
+// (2 x 4: 128 x 64 / 64 x 32 each), twice the waves per SIMD, so one wave's MFMAs cover another's
+// waits, against 1.5x the fragment reads (fp32: config 3's product 136 -> 146-147 TFLOP/s, the
+// 256 x 256 tile no longer spilling; the 3x3 convolution 157 -> 154 us; the MLP step 0.606-0.616
+// -> 0.601 ms).
 // Config 3's f16 product: 1001-1008 -> 1026-1034 TFLOP/s in one process, B read N-major
 // 1043-1047 -> 1085; config 4's f16 3x3 convolution 26.5 -> 25.5 us, 1x1 stride 2 12.8 -> 12.2 us.
 // (256 x 256 convolution tiles keep four: the gather's per-lane state would spill.)
@@ -1044,7 +1044,7 @@ int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C
     using I128 = std::integral_constant<int, 128>;
     using I256 = std::integral_constant<int, 256>;
     if (ts.bm == 256 && ts.bn == 256) {
-        if constexpr (DT != MX_FLOAT32 && Src::kStrided)     // (the gather's state would spill)
+        if constexpr ((DT != MX_FLOAT32 || (!BNN && !AMN)) && Src::kStrided)  // (conv: the gather's state would spill)
             if (kWide16) return go(I256{}, I256{}, std::integral_constant<int, 4>{});
         return go(I256{}, I256{}, I2{});
     }
