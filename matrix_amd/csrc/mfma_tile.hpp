@@ -8,7 +8,8 @@
 //
 // Tiling: a block computes a BM x BN tile of C (each 256 or 128) as 2 x WN waves of BM/2 x BN/WN
 // (BM/64 x BN/(32 WN) MFMA tiles of 32 x 32 per wave, fp32 accumulators): WN = 2 (256 threads),
-// or WN = 4 (512 threads) for 16-bit and K-major fp32 256 x 256 and 128 x 128 tiles.  A K step
+// or WN = 4 (512 threads) for 16-bit 256 x 256 and 128 x 128 tiles and fp32 ones with A K-major.
+// A K step
 // covers 64 bytes of each row (32 elements of 16-bit data, 16 of fp32); LDS holds two slots of a
 // K pair -- 128 bytes of every row of A and of Bt -- so every fetch is a whole 128-byte line
 // (half-line fetches doubled the L2 -> LDS traffic).  Direct global -> LDS loads (gfx950
@@ -374,14 +375,14 @@ __device__ __forceinline__ DmaOffsets<N> dma_offsets_nn(uint32_t cols_valid, uin
 
 // One K step (16 rows) of the N-major B tile through registers, element loads, zero past K; rows
 // 0 .. 15 of the slot.  Thread chunk q = tid + 256 j is row q / (BN / 4), columns 4 (q % (BN / 4)).
-template <int BN> constexpr int kTailChunksNN = 16 * BN / 4 / NTHREADS;
+template <int BN, int NT = NTHREADS> constexpr int kTailChunksNN = 16 * BN / 4 / NT;
 
-template <int BN>
-__device__ __forceinline__ void load_tile_guarded_nn(f4v (&r)[kTailChunksNN<BN>], const float* __restrict__ base,
+template <int BN, int NT = NTHREADS>
+__device__ __forceinline__ void load_tile_guarded_nn(f4v (&r)[(kTailChunksNN<BN, NT>)], const float* __restrict__ base,
                                                      uint32_t cols_valid, uint32_t ldk, uint32_t k0, uint32_t K) {
 #pragma unroll
-    for (int j = 0; j < kTailChunksNN<BN>; j++) {
-        const int q = threadIdx.x + NTHREADS * j;
+    for (int j = 0; j < kTailChunksNN<BN, NT>; j++) {
+        const int q = threadIdx.x + NT * j;
         const uint32_t k = k0 + (uint32_t)(q / (BN / 4));
         const uint32_t c = (uint32_t)(q % (BN / 4)) * 4;
 #pragma unroll
@@ -390,11 +391,11 @@ __device__ __forceinline__ void load_tile_guarded_nn(f4v (&r)[kTailChunksNN<BN>]
     }
 }
 
-template <int BN>
-__device__ __forceinline__ void store_tile_nn(char* lds, const f4v (&r)[kTailChunksNN<BN>]) {
+template <int BN, int NT = NTHREADS>
+__device__ __forceinline__ void store_tile_nn(char* lds, const f4v (&r)[(kTailChunksNN<BN, NT>)]) {
 #pragma unroll
-    for (int j = 0; j < kTailChunksNN<BN>; j++) {
-        const int q = threadIdx.x + NTHREADS * j;
+    for (int j = 0; j < kTailChunksNN<BN, NT>; j++) {
+        const int q = threadIdx.x + NT * j;
         *reinterpret_cast<f4v*>(lds + (q / (BN / 4)) * (BN * 4) + (q % (BN / 4)) * 16) = r[j];
     }
 }
@@ -730,7 +731,7 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
                                                              GemmArgs g, typename Src::Geom geo) {
     using S = typename MmaTraits<DT>::S;
     using CT = std::conditional_t<SPLIT, float, S>;    // element type written to Cv
-    static_assert(WN == 2 || (WN == 4 && (DT != MX_FLOAT32 || (!BNN && !AMN))), "eight waves: 16-bit or K-major fp32");
+    static_assert(WN == 2 || (WN == 4 && (DT != MX_FLOAT32 || !AMN)), "eight waves");
     constexpr int NW = 2 * WN, NT = 64 * NW;           // waves (2 along M, WN along N), threads
     constexpr int TM = BM / 64;                        // A tiles of 32 rows per wave
     constexpr int WNT = BN / (32 * WN);                // Bt tiles of 32 rows per wave
@@ -926,9 +927,9 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
         const S* Ablk = Abat + (uint64_t)m0 * g.lda;
         for (uint32_t kt = 2 * KP; kt < KT; kt++) {
             if constexpr (T32) {
-                f4v ra[kTailChunksNN<BM>];
-                load_tile_guarded_nn<BM>(ra, reinterpret_cast<const float*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
-                store_tile_nn<BM>(la0, ra);
+                f4v ra[kTailChunksNN<BM, NT>];
+                load_tile_guarded_nn<BM, NT>(ra, reinterpret_cast<const float*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
+                store_tile_nn<BM, NT>(la0, ra);
             } else if constexpr (AMN) {
                 uint4 ra[kTailChunksNN16<BM, NT>];
                 load_tile_guarded_nn16<BM, NT>(ra, reinterpret_cast<const uint16_t*>(Amn), rows_a, g.ka, kt * KSTEP, Klen);
@@ -939,9 +940,9 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
                 store_tile<BM, NT>(la0, ra);
             }
             if constexpr (NN32) {
-                f4v rb[kTailChunksNN<BN>];
-                load_tile_guarded_nn<BN>(rb, reinterpret_cast<const float*>(Bblk), rows_b, g.kb, kt * KSTEP, Klen);
-                store_tile_nn<BN>(lb0, rb);
+                f4v rb[kTailChunksNN<BN, NT>];
+                load_tile_guarded_nn<BN, NT>(rb, reinterpret_cast<const float*>(Bblk), rows_b, g.kb, kt * KSTEP, Klen);
+                store_tile_nn<BN, NT>(lb0, rb);
             } else if constexpr (NN16) {
                 uint4 rb[kTailChunksNN16<BN, NT>];
                 load_tile_guarded_nn16<BN, NT>(rb, Bblk, rows_b, g.kb, kt * KSTEP, Klen);
@@ -1007,11 +1008,11 @@ __global__ __launch_bounds__(128 * WN) void mfma_tile_kernel(void* __restrict__ 
 // on 128 x 128.
 struct TileShape { int bm, bn; };
 
-// 16-bit tiles and fp32 tiles with both operands K-major (256 x 256 and 128 x 128) run eight waves
-// (2 x 4: 128 x 64 / 64 x 32 each), twice the waves per SIMD, so one wave's MFMAs cover another's
-// waits, against 1.5x the fragment reads (fp32: config 3's product 136 -> 146-147 TFLOP/s, the
-// 256 x 256 tile no longer spilling; the 3x3 convolution 157 -> 154 us; the MLP step 0.606-0.616
-// -> 0.601 ms).
+// 16-bit tiles and fp32 tiles with A K-major (256 x 256 and 128 x 128) run eight waves (2 x 4:
+// 128 x 64 / 64 x 32 each), twice the waves per SIMD, so one wave's MFMAs cover another's waits,
+// against 1.5x the fragment reads (fp32: config 3's product 136 -> 146-147 TFLOP/s, with B
+// N-major 134 -> 144, the 256 x 256 tile no longer spilling; the 3x3 convolution 157 -> 154 us; the
+// MLP step 0.606-0.616 -> 0.601 ms).  fp32 with A M-major keeps four.
 // Config 3's f16 product: 1001-1008 -> 1026-1034 TFLOP/s in one process, B read N-major
 // 1043-1047 -> 1085; config 4's f16 3x3 convolution 26.5 -> 25.5 us, 1x1 stride 2 12.8 -> 12.2 us.
 // (256 x 256 convolution tiles keep four: the gather's per-lane state would spill.)
@@ -1044,7 +1045,7 @@ int launch_tile_kernel(TileShape ts, GemmArgs g, typename Src::Geom geo, void* C
     using I128 = std::integral_constant<int, 128>;
     using I256 = std::integral_constant<int, 256>;
     if (ts.bm == 256 && ts.bn == 256) {
-        if constexpr ((DT != MX_FLOAT32 || (!BNN && !AMN)) && Src::kStrided)  // (conv: the gather's state would spill)
+        if constexpr ((DT != MX_FLOAT32 || !AMN) && Src::kStrided)  // (conv: the gather's state would spill)
             if (kWide16) return go(I256{}, I256{}, std::integral_constant<int, 4>{});
         return go(I256{}, I256{}, I2{});
     }
