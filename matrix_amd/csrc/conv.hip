@@ -137,6 +137,333 @@ struct ConvSrc {
     }
 };
 
+// ------------------------------------------------------------------ weight-resident halo kernel
+// A "same" convolution (stride 1, each output extent equal to its input extent, 1 or 2 spatial
+// axes) of a 16-bit type, one group, channels padded to exactly one K pair (Cgp x 2 bytes = 128:
+// 64 channels), at most 9 kernel positions.  Output position m (flattened over batch and spatial
+// axes) then reads, at kernel position t, input pixel m + sh_t (sh_t = sum_d (k_d dil_d - pad_d)
+// x the pixel stride of axis d) whenever that tap lies inside the image, zeros otherwise.
+//
+// * The kernel stays in registers.  A workgroup of 4 waves owns a column group of 128 output
+//   channels; wave (wm, wn) holds the MFMA B fragments of channels 64 wn .. 64 wn + 63 over all of
+//   K for the workgroup's whole life (KP x 32 registers), loaded once through LDS.
+// * A tile is 64 consecutive output positions.  Its A operand for all KP taps is one halo: the
+//   input pixel rows m0 - rlo .. m0 + 63 + rhi, 128 bytes each, DMA'd once into one half of a
+//   two-tile LDS ring (178 rows for a 3 x 3 kernel over 56-pixel image rows, a third of the bytes
+//   of gathering every tap's 64 rows).  A fragment of tap t reads LDS row (m - m0) + rlo + sh_t,
+//   or a zero row for a tap off the image.  The next tile's halo lands while this one runs.
+// * Wave (wm, wn) computes output rows 32 wm .. + 31 x its 64 channels: per K block of 16, one
+//   1 KB A fragment read from LDS for two MFMAs.
+// * The previous tile's results are written at the top of the next one, before its DMA: each
+//   wave stages its 32 x 64 block in its own 4 KB of LDS and stores whole 128-byte row pieces (8
+//   rows per instruction) instead of 16 bytes of 32 rows per instruction from the fragments.
+//   One vmcnt(0) wait per tile then covers the stores and the DMA after a whole tile of MFMAs.
+namespace wres {
+constexpr int BM = 64;                          // output positions per tile
+constexpr int BNC = 128;                        // output channels per column group
+constexpr int WSLOT = BNC * tile::ROWB;         // one K pair of the group's kernel rows (16 KB)
+constexpr int MAX_KP = 9;
+constexpr int CAP = 512;                        // rows of one ring half (64 KB)
+constexpr int RING = CAP * tile::ROWB;
+constexpr int MAX_HALO = 376;                   // halo rows DMA'd per tile, at most
+constexpr int ZROW = 383 * tile::ROWB;          // a row of zeros (taps off the image)
+constexpr int STAGE = 384 * tile::ROWB;         // rows 384 .. 511: C staging, 4 KB per wave
+// The two ring halves are separate arrays, so the compiler can tell the halo DMA into one half
+// from the fragment reads of the other.  C staging lives in the current half: the compiler adds
+// no wait before an LDS access to an array that a pending DMA does not write only if some DMA
+// (here the completed one of the current tile) writes that array.  Before the loop the halves
+// stage the kernel rows: K pairs 0-3 in half 0, 4-7 in half 1, 8 in an array of its own.
+static_assert(MAX_KP * WSLOT <= 2 * RING + WSLOT, "kernel row staging");
+static_assert(2 * RING + WSLOT <= 160 * 1024, "LDS of a workgroup");
+constexpr int PREFETCH = 4;                     // A fragments in flight ahead of the MFMAs
+
+struct HaloGeom {
+    FastDiv s0, s1;                 // spatial extents (1-D: s0 = 1)
+    int32_t rlo;                    // halo rows before a tile's first position
+    uint32_t hrows;                 // halo rows DMA'd per tile (a multiple of 8, <= MAX_HALO)
+    uint32_t npix;                  // input pixel rows (batch x spatial)
+    int32_t sh[MAX_KP];             // per kernel position: pixel shift
+    int32_t dk0[MAX_KP], dk1[MAX_KP];   // per kernel position: offset along each axis
+    uint32_t on, os0, os1;          // output element strides: batch, axis 0, axis 1
+};
+
+template <int DT> struct FragT;
+template <> struct FragT<MX_FLOAT16> { using V = tile::h8v; };
+template <> struct FragT<MX_BFLOAT16> { using V = tile::b8v; };
+
+// MFMAs whose kernel fragment is read in place: column tile 0 from AGPRs, column tile 1 from
+// VGPRs (together the kernel slice is 288 registers, more than either file holds; as builtins the
+// compiler copied one of them across before every MFMA).  The first MFMA of a tile takes
+// srcC = 0.  The results are read by VALU instructions only after mfma_drain's wait states.
+#define MX_MFMA_ASM(BC)                                                                                  \
+    template <int DT>                                                                                    \
+    __device__ __forceinline__ void mma_first_##BC(tile::f16v& c, const typename FragT<DT>::V& b,         \
+                                                   const typename FragT<DT>::V& a) {                     \
+        if constexpr (DT == MX_FLOAT16)                                                                  \
+            asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&a"(c) : #BC(b), "v"(a));          \
+        else                                                                                             \
+            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&a"(c) : #BC(b), "v"(a));         \
+    }                                                                                                    \
+    template <int DT>                                                                                    \
+    __device__ __forceinline__ void mma_acc_##BC(tile::f16v& c, const typename FragT<DT>::V& b,           \
+                                                 const typename FragT<DT>::V& a) {                       \
+        if constexpr (DT == MX_FLOAT16)                                                                  \
+            asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : #BC(b), "v"(a));          \
+        else                                                                                             \
+            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : #BC(b), "v"(a));         \
+    }
+MX_MFMA_ASM(a)
+MX_MFMA_ASM(v)
+#undef MX_MFMA_ASM
+
+// 24 wait states after the last MFMA writing c0 / c1 (a 32x32 XDL result needs at most 19 before a
+// VALU instruction reads it); the accumulators pass through, so their readers come after.
+__device__ __forceinline__ void mfma_drain(tile::f16v& c0, tile::f16v& c1) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(c0), "+a"(c1));
+}
+
+// g.M output positions, g.N channels, g.K = KP x 64; g.tiles_m = ceil(M / 64).  Block b serves
+// column group b / bpc and, within it, tiles [j T / bpc, (j + 1) T / bpc) with j = b % bpc.
+template <int DT, int KP>
+__global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ xp,
+                                                        const uint16_t* __restrict__ wp, GemmArgs ga, HaloGeom hga,
+                                                        uint32_t bpc) {
+    using S = uint16_t;
+    using V = typename FragT<DT>::V;
+    constexpr int KB = 4 * KP;                  // K blocks of 16 elements
+    constexpr int PE = tile::ROWB / 2;          // elements per K pair
+    __shared__ __align__(16) char ring0[RING];
+    __shared__ __align__(16) char ring1[RING];
+    __shared__ __align__(16) char wtail[KP > 8 ? WSLOT : 16];
+    auto wslot = [&](int p) -> char* { return p < 4 ? ring0 + p * WSLOT : p < 8 ? ring1 + (p - 4) * WSLOT : wtail; };
+    // the arguments as plain values: lambdas that capture a by-value kernel argument struct make
+    // the compiler copy it to scratch memory
+    struct {
+        uint32_t M, N, K, tiles_m;
+    } g = {ga.M, ga.N, ga.K, ga.tiles_m};
+    struct {
+        FastDiv s0, s1;
+        int32_t rlo;
+        uint32_t hrows, npix, on, os0, os1;
+        int32_t sh[KP], dk0[KP], dk1[KP];
+    } hg;
+    hg.s0 = hga.s0;
+    hg.s1 = hga.s1;
+    hg.rlo = hga.rlo;
+    hg.hrows = hga.hrows;
+    hg.npix = hga.npix;
+    hg.on = hga.on;
+    hg.os0 = hga.os0;
+    hg.os1 = hga.os1;
+#pragma unroll
+    for (int p = 0; p < KP; p++) {
+        hg.sh[p] = hga.sh[p];
+        hg.dk0[p] = hga.dk0[p];
+        hg.dk1[p] = hga.dk1[p];
+    }
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1, r32 = lane & 31, h = lane >> 5;
+    const uint32_t cg = blockIdx.x / bpc, j = blockIdx.x - cg * bpc;
+    const uint32_t n0 = cg * BNC;
+    const uint32_t t_lo = (uint32_t)((uint64_t)j * g.tiles_m / bpc);
+    const uint32_t t_hi = (uint32_t)((uint64_t)(j + 1) * g.tiles_m / bpc);
+
+    // kernel rows of the column group -> LDS (pair p at p * WSLOT, 128 rows of 128 bytes) -> registers
+    const uint32_t rows_b = g.N - n0 < (uint32_t)BNC ? g.N - n0 : (uint32_t)BNC;
+    {
+        const S* wcg = wp + (uint64_t)n0 * g.K;
+        const auto ob = tile::dma_offsets<S, 4>(rows_b, g.K, wave, lane);
+#pragma unroll
+        for (int p = 0; p < KP; p++) tile::dma_rows<S, 4>(wslot(p), wcg, ob, (uint32_t)(p * PE), wave);
+    }
+    tile::wait_vmem<0>();
+    __syncthreads();
+    V bf[KB][2];
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int rb = 64 * wn + 32 * t + r32;
+            const char* src = wslot(kb / 4) + rb * tile::ROWB + tile::swz(rb, 2 * (kb % 4) + h) * 16;
+            if (t == 0) {                       // straight into AGPRs
+                const uint32_t addr = (uint32_t)(uintptr_t)src;
+                asm volatile("ds_read_b128 %0, %1" : "=a"(bf[kb][t]) : "v"(addr) : "memory");
+            } else {
+                bf[kb][t] = *reinterpret_cast<const V*>(src);
+            }
+        }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // (the compiler does not count the asm reads)
+    __syncthreads();                            // every wave holds its fragments: the ring is free
+    if (wave == 0 && lane < 16) *reinterpret_cast<uint4*>((lane < 8 ? ring0 : ring1) + ZROW + (lane % 8) * 16) = uint4{0, 0, 0, 0};
+
+#if __HIP_DEVICE_COMPILE__                               // (the buffer resource type is device-only)
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<S*>(xp), 0, (int)(hg.npix * (uint32_t)tile::ROWB), 0x00020000);
+#endif
+    // the halo of tile t: rows r = 0 .. hrows - 1 are input pixels m0 - rlo + r (clamped into the
+    // image: a clamped row is read only by taps off the image, which take the zero row); DMA
+    // instruction i fills rows 8 i .. 8 i + 7, lane L row 8 i + L / 8, stored chunk L % 8
+    auto issue_a = [&](uint32_t t, char* buf) __attribute__((always_inline)) {
+        const int32_t first = (int32_t)(t * BM) - hg.rlo;
+        const int nd = (int)(hg.hrows / 8);
+        for (int i = wave; i < nd; i += 4) {
+            const int r = 8 * i + lane / 8;
+            int32_t pix = first + r;
+            pix = pix < 0 ? 0 : (pix >= (int32_t)hg.npix ? (int32_t)hg.npix - 1 : pix);
+            const uint32_t off = (uint32_t)pix * (uint32_t)tile::ROWB + (uint32_t)tile::swz(r, lane % 8) * 16u;
+#if __HIP_DEVICE_COMPILE__
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(buf + i * 1024),
+                                                     16, off, 0, 0, 0);
+#else
+            (void)off;
+#endif
+        }
+    };
+    // acc[i][t]: C^T fragment of column tile t (lane: row r32 of the wave's 32, columns
+    // 32 t + 8 q + 4 h + e in register 4 q + e); i alternates between consecutive tiles
+    tile::f16v acc[2][2];
+    const uint32_t cw = n0 + 64 * wn;
+    const bool full_cols = cw + 64 <= g.N;
+    auto row_off = [&](uint32_t m) __attribute__((always_inline)) -> uint64_t {
+        const uint32_t q1 = hg.s1.div(m), o1 = m - q1 * hg.s1.d;
+        const uint32_t n = hg.s0.div(q1), o0 = q1 - n * hg.s0.d;
+        return (uint64_t)n * hg.on + (uint64_t)o0 * hg.os0 + (uint64_t)o1 * hg.os1;
+    };
+    auto cvt = [](float v) __attribute__((always_inline)) -> uint16_t {
+        return DT == MX_FLOAT16 ? float_to_half_bits(v) : float_to_bf16(v);
+    };
+    // staged store of a finished tile (the wave's 32 rows x 64 channels), in 13 pieces: 8 that
+    // write its fragments to the wave's 4 KB of LDS (piece j: column tile j / 4, registers
+    // 4 (j % 4) ..; chunk k of row r at (k ^ (r & 7)) * 16), a compiler fence, then 4 that each
+    // read 8 whole rows back and store them (64 lanes x 16 bytes: 8 row pieces of 128 bytes).
+    // A wave's LDS accesses complete in order, so the reads see the writes.  Stage and rows read
+    // are this wave's own; the barrier at the top of the next tile orders them against the DMA.
+    typedef unsigned u4v __attribute__((ext_vector_type(4)));
+    auto store_piece = [&](char* stage, const tile::f16v (&c)[2], uint32_t mw, int j) __attribute__((always_inline)) {
+        if (j < 8) {
+            const int tt = j / 4, q = j % 4, k = 4 * tt + q;
+            uint2 u;
+            u.x = (uint32_t)cvt(c[tt][4 * q]) | ((uint32_t)cvt(c[tt][4 * q + 1]) << 16);
+            u.y = (uint32_t)cvt(c[tt][4 * q + 2]) | ((uint32_t)cvt(c[tt][4 * q + 3]) << 16);
+            // (as inline asm: the compiler waited for the pending halo DMA before this write, which
+            // goes to rows that DMA never touches)
+            const uint32_t addr = (uint32_t)(uintptr_t)(stage + r32 * tile::ROWB + ((k ^ (r32 & 7)) * 16) + 8 * h);
+            asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(u) : "memory");
+        } else if (j == 8) {
+            asm volatile("" ::: "memory");
+        } else {
+            const int it = j - 9, k = lane % 8, rr = 8 * it + lane / 8;
+            const u4v v = *reinterpret_cast<const u4v*>(stage + rr * tile::ROWB + ((k ^ (rr & 7)) * 16));
+            if (mw + rr < g.M)
+                __builtin_nontemporal_store(v, reinterpret_cast<u4v*>(out + row_off(mw + rr) + cw + 8 * k));
+        }
+    };
+    constexpr int PIECES = 13;
+    // a column group's last wave may hold fewer than 64 channels: element stores from the fragments
+    auto store_edge = [&](const tile::f16v (&c)[2], uint32_t t) __attribute__((always_inline)) {
+        const uint32_t row = t * BM + 32 * wm + r32;
+        if (row >= g.M) return;
+        S* crow = out + row_off(row);
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t col = cw + 32 * tt + 8 * q + 4 * h + e;
+                    if (col < g.N) crow[col] = cvt(c[tt][4 * q + e]);
+                }
+    };
+    auto store_all = [&](auto full, const tile::f16v (&c)[2], uint32_t t) __attribute__((always_inline)) {
+        if constexpr (decltype(full)::value) {
+#pragma unroll
+            for (int j = 0; j < PIECES; j++) store_piece(ring0 + STAGE + wave * 4096, c, t * BM + 32 * wm, j);
+        } else {
+            store_edge(c, t);
+        }
+    };
+    // Tile t from ring half P; with HP, tile t - 1's results (acc[1 - P]) are stored meanwhile --
+    // with FULL in pieces between its MFMAs (a wave is alone on its SIMD, so an epilogue before
+    // them would leave the matrix core idle), otherwise before them.
+    auto step = [&](auto par, auto has_prev, auto full, uint32_t t) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        constexpr bool HP = decltype(has_prev)::value, FULL = decltype(full)::value;
+        char* cur = P == 0 ? ring0 : ring1;
+        char* nxt = P == 0 ? ring1 : ring0;
+        char* stage = cur + STAGE + wave * 4096;
+        tile::wait_vmem<0>();                   // this wave's DMA of tile t (and its last stores)
+        tile::ring_barrier();                   // every wave's DMA of t landed; t - 1's reads done
+        if (t + 1 < t_hi) issue_a(t + 1, nxt);
+        if constexpr (HP && !FULL) store_edge(acc[1 - P], t - 1);
+        // per tap: the LDS byte offset of this lane's A row (its output position's tap pixel, or
+        // the zero row) and that row's chunk swizzle
+        const uint32_t m = t * BM + 32 * wm + r32;
+        const uint32_t q1 = hg.s1.div(m), o1 = m - q1 * hg.s1.d;
+        const uint32_t o0 = q1 - hg.s0.div(q1) * hg.s0.d;
+        const int base = 32 * wm + r32 + hg.rlo;
+        int roff[KP], rsw[KP];
+#pragma unroll
+        for (int p = 0; p < KP; p++) {
+            const bool ok = (uint32_t)((int32_t)o0 + hg.dk0[p]) < hg.s0.d && (uint32_t)((int32_t)o1 + hg.dk1[p]) < hg.s1.d;
+            const int row = base + hg.sh[p];
+            roff[p] = ok ? row * tile::ROWB : ZROW;
+            rsw[p] = ok ? (row >> 1) & 7 : 0;
+        }
+        auto rd = [&](int kb) __attribute__((always_inline)) -> V {
+            const int p = kb / 4;
+            return *reinterpret_cast<const V*>(cur + roff[p] + (((2 * (kb % 4) + h) ^ rsw[p]) * 16));
+        };
+        const uint32_t mw = (t - 1) * BM + 32 * wm;     // tile t - 1's first row of this wave (HP)
+        V a[PREFETCH];
+#pragma unroll
+        for (int i = 0; i < PREFETCH; i++) a[i] = rd(i);
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+            if (kb == 0) {
+                mma_first_a<DT>(acc[P][0], bf[kb][0], a[kb % PREFETCH]);
+                mma_first_v<DT>(acc[P][1], bf[kb][1], a[kb % PREFETCH]);
+            } else {
+                mma_acc_a<DT>(acc[P][0], bf[kb][0], a[kb % PREFETCH]);
+                mma_acc_v<DT>(acc[P][1], bf[kb][1], a[kb % PREFETCH]);
+            }
+            if (kb + PREFETCH < KB) a[kb % PREFETCH] = rd(kb + PREFETCH);
+            if constexpr (HP && FULL) {
+                // piece j goes after the MFMAs of K block min(j + 1, KB - 1)
+#pragma unroll
+                for (int j = 0; j < PIECES; j++)
+                    if ((j + 1 < KB ? j + 1 : KB - 1) == kb) store_piece(stage, acc[1 - P], mw, j);
+            }
+        }
+        mfma_drain(acc[P][0], acc[P][1]);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using BF = std::false_type;
+    using BT = std::true_type;
+    auto run = [&](auto full) __attribute__((always_inline)) {
+        uint32_t t = t_lo;
+        step(I0{}, BF{}, full, t);
+        for (;;) {
+            if (++t >= t_hi) {
+                store_all(full, acc[0], t - 1);
+                break;
+            }
+            step(I1{}, BT{}, full, t);
+            if (++t >= t_hi) {
+                store_all(full, acc[1], t - 1);
+                break;
+            }
+            step(I0{}, BT{}, full, t);
+        }
+    };
+    if (t_lo >= t_hi) return;                   // (uniform over the block)
+    issue_a(t_lo, ring0);
+    if (full_cols) run(BT{});
+    else run(BF{});
+}
+}  // namespace wres
+
 // ------------------------------------------------------------------ packing
 struct ConvShape {
     int ns;
@@ -570,6 +897,93 @@ int launch_pack_kernel(const ConvShape& cs, uint32_t Cgp, int flip, S* wp, const
     return MX_OK;
 }
 
+// The weight-resident halo kernel: one workgroup per CU, the column groups side by side, each
+// group's blocks over contiguous tile ranges (neighbouring tiles share most of their halo rows in
+// the L2).  MATRIX_AMD_CONV_HALO=0 takes the tile kernel instead.
+bool halo_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("MATRIX_AMD_CONV_HALO");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// The halo geometry of a same convolution, or false when the halo kernel does not apply: one
+// group, 64 channels per K pair (16-bit), at most 9 kernel positions, stride 1 and each output
+// extent equal to its input extent, the halo within a ring half, C rows in whole 16-byte units.
+template <int NS>
+bool halo_geom(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, const int* stride, const int* dil,
+               wres::HaloGeom& hg) {
+    if (cs.groups != 1 || Cgp * 2 != (uint32_t)tile::ROWB || cs.out_s[NS + 1] != 1) return false;
+    uint32_t kpos = 1;
+    for (int d = 0; d < NS; d++) {
+        if (stride[d] != 1 || cs.OS[d] != cs.S[d]) return false;
+        kpos *= cs.K[d];
+    }
+    if (kpos > (uint32_t)wres::MAX_KP) return false;
+    for (int a = 0; a <= NS; a++)
+        if ((cs.out_s[a] * 2) % 16) return false;
+    hg = wres::HaloGeom{};
+    const uint32_t S0 = NS == 2 ? cs.S[0] : 1, S1 = cs.S[NS - 1];
+    const uint32_t K0 = NS == 2 ? cs.K[0] : 1, K1 = cs.K[NS - 1];
+    const int d0 = NS == 2 ? dil[0] : 1, d1 = dil[NS - 1];
+    const int p0 = NS == 2 ? pad_lo[0] : 0, p1 = pad_lo[NS - 1];
+    int64_t lo = 0, hi = 0;
+    for (uint32_t k0 = 0; k0 < K0; k0++)
+        for (uint32_t k1 = 0; k1 < K1; k1++) {
+            const uint32_t t = k0 * K1 + k1;
+            const int64_t a0 = (int64_t)k0 * d0 - p0, a1 = (int64_t)k1 * d1 - p1;
+            const int64_t sh = a0 * S1 + a1;
+            if (sh < lo) lo = sh;
+            if (sh > hi) hi = sh;
+            hg.dk0[t] = (int32_t)a0;
+            hg.dk1[t] = (int32_t)a1;
+            hg.sh[t] = (int32_t)sh;
+        }
+    const int64_t rows = (wres::BM + (-lo) + hi + 7) / 8 * 8;
+    if (rows > wres::MAX_HALO) return false;
+    hg.s0 = FastDiv(S0);
+    hg.s1 = FastDiv(S1);
+    hg.rlo = (int32_t)(-lo);
+    hg.hrows = (uint32_t)rows;
+    hg.npix = (uint32_t)((uint64_t)cs.N * S0 * S1);
+    hg.on = (uint32_t)cs.out_s[0];
+    hg.os0 = NS == 2 ? (uint32_t)cs.out_s[1] : 0;
+    hg.os1 = (uint32_t)cs.out_s[NS];
+    return true;
+}
+
+template <int DT>
+int launch_halo(GemmArgs g, const wres::HaloGeom& hg, void* out, const void* xp, const void* wp, hipStream_t st) {
+    const uint32_t kp = g.K / (tile::ROWB / 2);
+    g.tiles_m = (g.M + wres::BM - 1) / wres::BM;
+    const uint32_t cgs = (g.N + wres::BNC - 1) / wres::BNC;
+    uint32_t bpc = cgs >= 256 ? 1 : 256 / cgs;
+    if (bpc > g.tiles_m) bpc = g.tiles_m;
+    const uint64_t blocks = (uint64_t)cgs * bpc;
+    if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: grid too large");
+    auto go = [&](auto kpc) -> int {
+        constexpr int KP = decltype(kpc)::value;
+        hipLaunchKernelGGL((wres::conv_halo_kernel<DT, KP>), dim3((uint32_t)blocks), dim3(256), 0, st,
+                           static_cast<uint16_t*>(out), static_cast<const uint16_t*>(xp),
+                           static_cast<const uint16_t*>(wp), g, hg, bpc);
+        MX_HIP(hipGetLastError());
+        return MX_OK;
+    };
+    switch (kp) {
+    case 1: return go(std::integral_constant<int, 1>{});
+    case 2: return go(std::integral_constant<int, 2>{});
+    case 3: return go(std::integral_constant<int, 3>{});
+    case 4: return go(std::integral_constant<int, 4>{});
+    case 5: return go(std::integral_constant<int, 5>{});
+    case 6: return go(std::integral_constant<int, 6>{});
+    case 7: return go(std::integral_constant<int, 7>{});
+    case 8: return go(std::integral_constant<int, 8>{});
+    case 9: return go(std::integral_constant<int, 9>{});
+    default: return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: halo kernel past 9 kernel positions");
+    }
+}
+
 template <int DT, int NS>
 int launch_implicit_gemm(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, const int* stride, const int* dil,
                          void* out, const void* xp, const void* wp, hipStream_t st) {
@@ -614,6 +1028,11 @@ int launch_implicit_gemm(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, c
         g.bd.sA[0] = Cgp;
         g.bd.sB[0] = cs.Og * g.K;
         g.bd.sC[0] = (uint32_t)(cs.Og * cs.out_s[NS + 1]);
+    }
+    if constexpr (DT != MX_FLOAT32) {
+        wres::HaloGeom hg;
+        if ((uintptr_t)out % 16 == 0 && halo_enabled() && halo_geom<NS>(cs, Cgp, pad_lo, stride, dil, hg))
+            return launch_halo<DT>(g, hg, out, xp, wp, st);
     }
     return tile::launch_tile_kernel<DT, true, false, ConvSrc<NS>>(tile::choose_tile(g.M, g.N, g.batches), g, geo,
                                                                   out, xp, wp, st, "mx_launch_conv_nd");

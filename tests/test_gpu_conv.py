@@ -213,6 +213,41 @@ def test_conv2d_many_tiles(mx, orc, dt, case):
     assert err <= TOL[dt], (dt, case, err)
 
 
+@pytest.mark.parametrize("dt", ["FLOAT16", "BFLOAT16"])
+@pytest.mark.parametrize("case", [
+    # (N, H, W, C, O, kh, kw, pad, dil): same convolutions (stride 1, output extents = input
+    # extents) over at most 64 channels and 9 kernel positions -- the weight-resident halo kernel.
+    # O a multiple of 128 takes its staged whole-row stores; others its per-element edge stores.
+    (4, 30, 70, 64, 128, 3, 3, 1, 1),      # 8400 positions: 132 tiles, the last one 16 rows
+    (5, 64, 64, 64, 128, 1, 3, 1, 1),      # 320 tiles: blocks walk two tiles through the ring
+    (1, 20, 21, 48, 256, 3, 3, 2, 2),      # dilation 2, two full column groups, 48 -> 64 channels
+    (1, 6, 200, 64, 128, 3, 3, 1, 1),      # 200-pixel rows: a 472-row halo per tile
+    (2, 13, 17, 64, 200, 3, 3, 1, 1),      # a full column group and a 72-channel one
+])
+def test_conv2d_same_halo(mx, orc, dt, case):
+    code = getattr(mx, dt)
+    n, h, w, c, o, kh, kw, pad, dil = case
+    rng = np.random.default_rng(n * 131 + h * 17 + w + c + o + kw)
+    x = store_of(code, rng.standard_normal([n, h, w, c]).astype(np.float32), mx)
+    wt = store_of(code, (rng.standard_normal([o, kh, kw, c]) * np.sqrt(2.0 / (c * kh * kw))).astype(np.float32), mx)
+    pads = [pad if kh > 1 else 0, pad if kw > 1 else 0]
+    got, ref = run_conv(mx, orc, code, x, [n, h, w, c], contiguous_strides([n, h, w, c]), wt, [o, kh, kw, c],
+                        contiguous_strides([o, kh, kw, c]), pads, [1, 1], dil=[dil, dil])
+    assert got.size == n * h * w * o
+    err = normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx))
+    assert err <= TOL[dt], (dt, case, err)
+
+
+def test_conv1d_same_halo_full_columns(mx, orc):
+    code = mx.FLOAT16
+    rng = np.random.default_rng(12)
+    x = store_of(code, rng.standard_normal([3, 200, 64]).astype(np.float32), mx)
+    wt = store_of(code, (rng.standard_normal([128, 5, 64]) * 0.1).astype(np.float32), mx)
+    got, ref = run_conv(mx, orc, code, x, [3, 200, 64], contiguous_strides([3, 200, 64]), wt, [128, 5, 64],
+                        contiguous_strides([128, 5, 64]), [2], [1])
+    assert normwise_rel(as_f32(code, got, mx), as_f32(code, ref, mx)) <= TOL["FLOAT16"]
+
+
 def test_conv1d_many_tiles(mx, orc):
     code = mx.FLOAT16
     rng = np.random.default_rng(11)
