@@ -144,20 +144,20 @@ struct ConvSrc {
 // axes) then reads, at kernel position t, input pixel m + sh_t (sh_t = sum_d (k_d dil_d - pad_d)
 // x the pixel stride of axis d) whenever that tap lies inside the image, zeros otherwise.
 //
-// * The kernel stays in registers.  A workgroup of 4 waves owns a column group of 128 output
-//   channels; wave (wm, wn) holds the MFMA B fragments of channels 64 wn .. 64 wn + 63 over all of
-//   K for the workgroup's whole life (KP x 32 registers), loaded once through LDS.
+// * The kernel stays in registers.  A workgroup of 8 waves (two per SIMD) owns a column group of
+//   128 output channels; wave (wm, wn) holds the MFMA B fragments of channels 32 wn .. 32 wn + 31
+//   over all of K for the workgroup's whole life (KP x 16 registers), loaded once through LDS.
 // * A tile is 64 consecutive output positions.  Its A operand for all KP taps is one halo: the
 //   input pixel rows m0 - rlo .. m0 + 63 + rhi, 128 bytes each, DMA'd once into one half of a
 //   two-tile LDS ring (178 rows for a 3 x 3 kernel over 56-pixel image rows, a third of the bytes
 //   of gathering every tap's 64 rows).  A fragment of tap t reads LDS row (m - m0) + rlo + sh_t,
 //   or a zero row for a tap off the image.  The next tile's halo lands while this one runs.
-// * Wave (wm, wn) computes output rows 32 wm .. + 31 x its 64 channels: per K block of 16, one
-//   1 KB A fragment read from LDS for two MFMAs.
-// * The previous tile's results are written at the top of the next one, before its DMA: each
-//   wave stages its 32 x 64 block in its own 4 KB of LDS and stores whole 128-byte row pieces (8
-//   rows per instruction) instead of 16 bytes of 32 rows per instruction from the fragments.
-//   One vmcnt(0) wait per tile then covers the stores and the DMA after a whole tile of MFMAs.
+// * Wave (wm, wn) computes output rows 32 wm .. + 31 x its 32 channels: per K block of 16, one
+//   1 KB A fragment read from LDS for one MFMA.
+// * The previous tile's results, rounded to 16 bits, are stored in pieces between the current
+//   tile's MFMAs: each wave stages its 32 x 32 block in its own 2 KB of LDS and stores 64-byte
+//   row pieces (16 rows per instruction) instead of 16 bytes of 32 rows per instruction from the
+//   fragment.  One vmcnt(0) wait per tile covers the stores and the DMA.
 namespace wres {
 constexpr int BM = 64;                          // output positions per tile
 constexpr int BNC = 128;                        // output channels per column group
@@ -167,12 +167,11 @@ constexpr int CAP = 512;                        // rows of one ring half (64 KB)
 constexpr int RING = CAP * tile::ROWB;
 constexpr int MAX_HALO = 376;                   // halo rows DMA'd per tile, at most
 constexpr int ZROW = 383 * tile::ROWB;          // a row of zeros (taps off the image)
-constexpr int STAGE = 384 * tile::ROWB;         // rows 384 .. 511: C staging, 4 KB per wave
+constexpr int STAGE = 384 * tile::ROWB;         // rows 384 .. 511: C staging, 2 KB per wave
 // The two ring halves are separate arrays, so the compiler can tell the halo DMA into one half
-// from the fragment reads of the other.  C staging lives in the current half: the compiler adds
-// no wait before an LDS access to an array that a pending DMA does not write only if some DMA
-// (here the completed one of the current tile) writes that array.  Before the loop the halves
-// stage the kernel rows: K pairs 0-3 in half 0, 4-7 in half 1, 8 in an array of its own.
+// from the fragment reads of the other and adds no wait for it.  C staging uses rows of the
+// current half that the DMA never writes.  Before the loop the halves stage the kernel rows: K
+// pairs 0-3 in half 0, 4-7 in half 1, 8 in an array of its own.
 static_assert(MAX_KP * WSLOT <= 2 * RING + WSLOT, "kernel row staging");
 static_assert(2 * RING + WSLOT <= 160 * 1024, "LDS of a workgroup");
 constexpr int PREFETCH = 4;                     // A fragments in flight ahead of the MFMAs
@@ -191,45 +190,27 @@ template <int DT> struct FragT;
 template <> struct FragT<MX_FLOAT16> { using V = tile::h8v; };
 template <> struct FragT<MX_BFLOAT16> { using V = tile::b8v; };
 
-// MFMAs whose kernel fragment is read in place: column tile 0 from AGPRs, column tile 1 from
-// VGPRs (together the kernel slice is 288 registers, more than either file holds; as builtins the
-// compiler copied one of them across before every MFMA).  The first MFMA of a tile takes
-// srcC = 0.  The results are read by VALU instructions only after mfma_drain's wait states.
-#define MX_MFMA_ASM(BC)                                                                                  \
-    template <int DT>                                                                                    \
-    __device__ __forceinline__ void mma_first_##BC(tile::f16v& c, const typename FragT<DT>::V& b,         \
-                                                   const typename FragT<DT>::V& a) {                     \
-        if constexpr (DT == MX_FLOAT16)                                                                  \
-            asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&a"(c) : #BC(b), "v"(a));          \
-        else                                                                                             \
-            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&a"(c) : #BC(b), "v"(a));         \
-    }                                                                                                    \
-    template <int DT>                                                                                    \
-    __device__ __forceinline__ void mma_acc_##BC(tile::f16v& c, const typename FragT<DT>::V& b,           \
-                                                 const typename FragT<DT>::V& a) {                       \
-        if constexpr (DT == MX_FLOAT16)                                                                  \
-            asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(c) : #BC(b), "v"(a));          \
-        else                                                                                             \
-            asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : #BC(b), "v"(a));         \
-    }
-MX_MFMA_ASM(a)
-MX_MFMA_ASM(v)
-#undef MX_MFMA_ASM
-
-// 24 wait states after the last MFMA writing c0 / c1 (a 32x32 XDL result needs at most 19 before a
-// VALU instruction reads it); the accumulators pass through, so their readers come after.
-__device__ __forceinline__ void mfma_drain(tile::f16v& c0, tile::f16v& c1) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+a"(c0), "+a"(c1));
+template <int DT>
+__device__ __forceinline__ tile::f16v mma(const typename FragT<DT>::V& b, const typename FragT<DT>::V& a,
+                                          const tile::f16v& c) {
+    if constexpr (DT == MX_FLOAT16) return __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
 }
 
 // g.M output positions, g.N channels, g.K = KP x 64; g.tiles_m = ceil(M / 64).  Block b serves
 // column group b / bpc and, within it, tiles [j T / bpc, (j + 1) T / bpc) with j = b % bpc.
+// Eight waves, two per SIMD: wave (wm, wn) computes output rows 32 wm .. + 31 x channels
+// 32 wn .. + 31 of the group and holds those channels' kernel fragments (KP x 16 registers).  One
+// wave per SIMD holding 64 channels (two MFMAs per A fragment read) kept the matrix cores busy
+// only about half the time: a lone wave's MFMAs issue one after another with gaps that a second
+// wave fills.
 template <int DT, int KP>
-__global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ xp,
+__global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ xp,
                                                         const uint16_t* __restrict__ wp, GemmArgs ga, HaloGeom hga,
                                                         uint32_t bpc) {
     using S = uint16_t;
     using V = typename FragT<DT>::V;
+    constexpr int NW = 8;                       // waves
     constexpr int KB = 4 * KP;                  // K blocks of 16 elements
     constexpr int PE = tile::ROWB / 2;          // elements per K pair
     __shared__ __align__(16) char ring0[RING];
@@ -263,37 +244,28 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ o
     }
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1, r32 = lane & 31, h = lane >> 5;
+    const int wm = wave >> 2, wn = wave & 3, r32 = lane & 31, h = lane >> 5;
     const uint32_t cg = blockIdx.x / bpc, j = blockIdx.x - cg * bpc;
     const uint32_t n0 = cg * BNC;
     const uint32_t t_lo = (uint32_t)((uint64_t)j * g.tiles_m / bpc);
     const uint32_t t_hi = (uint32_t)((uint64_t)(j + 1) * g.tiles_m / bpc);
 
-    // kernel rows of the column group -> LDS (pair p at p * WSLOT, 128 rows of 128 bytes) -> registers
+    // kernel rows of the column group -> LDS (pair p in wslot(p), 128 rows of 128 bytes) -> registers
     const uint32_t rows_b = g.N - n0 < (uint32_t)BNC ? g.N - n0 : (uint32_t)BNC;
     {
         const S* wcg = wp + (uint64_t)n0 * g.K;
-        const auto ob = tile::dma_offsets<S, 4>(rows_b, g.K, wave, lane);
+        const auto ob = tile::dma_offsets<S, 2>(rows_b, g.K, wave, lane);
 #pragma unroll
-        for (int p = 0; p < KP; p++) tile::dma_rows<S, 4>(wslot(p), wcg, ob, (uint32_t)(p * PE), wave);
+        for (int p = 0; p < KP; p++) tile::dma_rows<S, 2>(wslot(p), wcg, ob, (uint32_t)(p * PE), wave);
     }
     tile::wait_vmem<0>();
     __syncthreads();
-    V bf[KB][2];
+    V bf[KB];
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++)
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int rb = 64 * wn + 32 * t + r32;
-            const char* src = wslot(kb / 4) + rb * tile::ROWB + tile::swz(rb, 2 * (kb % 4) + h) * 16;
-            if (t == 0) {                       // straight into AGPRs
-                const uint32_t addr = (uint32_t)(uintptr_t)src;
-                asm volatile("ds_read_b128 %0, %1" : "=a"(bf[kb][t]) : "v"(addr) : "memory");
-            } else {
-                bf[kb][t] = *reinterpret_cast<const V*>(src);
-            }
-        }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // (the compiler does not count the asm reads)
+    for (int kb = 0; kb < KB; kb++) {
+        const int rb = 32 * wn + r32;
+        bf[kb] = *reinterpret_cast<const V*>(wslot(kb / 4) + rb * tile::ROWB + tile::swz(rb, 2 * (kb % 4) + h) * 16);
+    }
     __syncthreads();                            // every wave holds its fragments: the ring is free
     if (wave == 0 && lane < 16) *reinterpret_cast<uint4*>((lane < 8 ? ring0 : ring1) + ZROW + (lane % 8) * 16) = uint4{0, 0, 0, 0};
 
@@ -307,7 +279,7 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ o
     auto issue_a = [&](uint32_t t, char* buf) __attribute__((always_inline)) {
         const int32_t first = (int32_t)(t * BM) - hg.rlo;
         const int nd = (int)(hg.hrows / 8);
-        for (int i = wave; i < nd; i += 4) {
+        for (int i = wave; i < nd; i += NW) {
             const int r = 8 * i + lane / 8;
             int32_t pix = first + r;
             pix = pix < 0 ? 0 : (pix >= (int32_t)hg.npix ? (int32_t)hg.npix - 1 : pix);
@@ -320,11 +292,13 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ o
 #endif
         }
     };
-    // acc[i][t]: C^T fragment of column tile t (lane: row r32 of the wave's 32, columns
-    // 32 t + 8 q + 4 h + e in register 4 q + e); i alternates between consecutive tiles
-    tile::f16v acc[2][2];
-    const uint32_t cw = n0 + 64 * wn;
-    const bool full_cols = cw + 64 <= g.N;
+    // acc: the tile as a C^T fragment (lane: row r32 of the wave's 32, columns 8 q + 4 h + e in
+    // register 4 q + e); prev: the finished previous tile rounded to 16 bits, two columns a word
+    // (word 2 q + i: columns 8 q + 4 h + 2 i, + 1), stored during the next tile's MFMAs
+    tile::f16v acc;
+    uint32_t prev[8];
+    const uint32_t cw = n0 + 32 * wn;
+    const bool full_cols = cw + 32 <= g.N;
     auto row_off = [&](uint32_t m) __attribute__((always_inline)) -> uint64_t {
         const uint32_t q1 = hg.s1.div(m), o1 = m - q1 * hg.s1.d;
         const uint32_t n = hg.s0.div(q1), o0 = q1 - n * hg.s0.d;
@@ -333,69 +307,66 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ o
     auto cvt = [](float v) __attribute__((always_inline)) -> uint16_t {
         return DT == MX_FLOAT16 ? float_to_half_bits(v) : float_to_bf16(v);
     };
-    // staged store of a finished tile (the wave's 32 rows x 64 channels), in 13 pieces: 8 that
-    // write its fragments to the wave's 4 KB of LDS (piece j: column tile j / 4, registers
-    // 4 (j % 4) ..; chunk k of row r at (k ^ (r & 7)) * 16), a compiler fence, then 4 that each
-    // read 8 whole rows back and store them (64 lanes x 16 bytes: 8 row pieces of 128 bytes).
-    // A wave's LDS accesses complete in order, so the reads see the writes.  Stage and rows read
-    // are this wave's own; the barrier at the top of the next tile orders them against the DMA.
+    // staged store of a finished tile (the wave's 32 rows x 32 channels, 64 bytes a row), in 7
+    // pieces: 4 that write its fragment to the wave's 2 KB of LDS (piece q: registers 4 q ..;
+    // chunk k of row r at (k ^ (r & 3)) * 16), a compiler fence, then 2 that each read 16 rows back
+    // and store them (64 lanes x 16 bytes).  A wave's LDS accesses complete in order, so the reads
+    // see the writes; stage and rows are this wave's own, and the barrier at the top of the next
+    // tile orders them against the DMA.
     typedef unsigned u4v __attribute__((ext_vector_type(4)));
-    auto store_piece = [&](char* stage, const tile::f16v (&c)[2], uint32_t mw, int j) __attribute__((always_inline)) {
-        if (j < 8) {
-            const int tt = j / 4, q = j % 4, k = 4 * tt + q;
+    auto store_piece = [&](char* stage, const uint32_t (&c)[8], uint32_t mw, int j) __attribute__((always_inline)) {
+        if (j < 4) {
+            const int q = j;
             uint2 u;
-            u.x = (uint32_t)cvt(c[tt][4 * q]) | ((uint32_t)cvt(c[tt][4 * q + 1]) << 16);
-            u.y = (uint32_t)cvt(c[tt][4 * q + 2]) | ((uint32_t)cvt(c[tt][4 * q + 3]) << 16);
+            u.x = c[2 * q];
+            u.y = c[2 * q + 1];
             // (as inline asm: the compiler waited for the pending halo DMA before this write, which
             // goes to rows that DMA never touches)
-            const uint32_t addr = (uint32_t)(uintptr_t)(stage + r32 * tile::ROWB + ((k ^ (r32 & 7)) * 16) + 8 * h);
+            const uint32_t addr = (uint32_t)(uintptr_t)(stage + r32 * 64 + ((q ^ (r32 & 3)) * 16) + 8 * h);
             asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(u) : "memory");
-        } else if (j == 8) {
+        } else if (j == 4) {
             asm volatile("" ::: "memory");
         } else {
-            const int it = j - 9, k = lane % 8, rr = 8 * it + lane / 8;
-            const u4v v = *reinterpret_cast<const u4v*>(stage + rr * tile::ROWB + ((k ^ (rr & 7)) * 16));
+            const int it = j - 5, k = lane % 4, rr = 16 * it + lane / 4;
+            const u4v v = *reinterpret_cast<const u4v*>(stage + rr * 64 + ((k ^ (rr & 3)) * 16));
             if (mw + rr < g.M)
                 __builtin_nontemporal_store(v, reinterpret_cast<u4v*>(out + row_off(mw + rr) + cw + 8 * k));
         }
     };
-    constexpr int PIECES = 13;
-    // a column group's last wave may hold fewer than 64 channels: element stores from the fragments
-    auto store_edge = [&](const tile::f16v (&c)[2], uint32_t t) __attribute__((always_inline)) {
+    constexpr int PIECES = 7;
+    // a column group's last waves may hold fewer than 32 channels: element stores from the fragment
+    auto store_edge = [&](const uint32_t (&c)[8], uint32_t t) __attribute__((always_inline)) {
         const uint32_t row = t * BM + 32 * wm + r32;
         if (row >= g.M) return;
         S* crow = out + row_off(row);
 #pragma unroll
-        for (int tt = 0; tt < 2; tt++)
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint32_t col = cw + 32 * tt + 8 * q + 4 * h + e;
-                    if (col < g.N) crow[col] = cvt(c[tt][4 * q + e]);
-                }
+            for (int e = 0; e < 4; e++) {
+                const uint32_t col = cw + 8 * q + 4 * h + e;
+                if (col < g.N) crow[col] = (uint16_t)(c[2 * q + e / 2] >> (16 * (e % 2)));
+            }
     };
-    auto store_all = [&](auto full, const tile::f16v (&c)[2], uint32_t t) __attribute__((always_inline)) {
+    auto store_all = [&](auto full, const uint32_t (&c)[8], uint32_t t) __attribute__((always_inline)) {
         if constexpr (decltype(full)::value) {
 #pragma unroll
-            for (int j = 0; j < PIECES; j++) store_piece(ring0 + STAGE + wave * 4096, c, t * BM + 32 * wm, j);
+            for (int j = 0; j < PIECES; j++) store_piece(ring0 + STAGE + wave * 2048, c, t * BM + 32 * wm, j);
         } else {
             store_edge(c, t);
         }
     };
-    // Tile t from ring half P; with HP, tile t - 1's results (acc[1 - P]) are stored meanwhile --
-    // with FULL in pieces between its MFMAs (a wave is alone on its SIMD, so an epilogue before
-    // them would leave the matrix core idle), otherwise before them.
+    // Tile t from ring half P; with HP, tile t - 1's results (prev) are stored meanwhile -- with
+    // FULL in pieces between its MFMAs, otherwise before them.
     auto step = [&](auto par, auto has_prev, auto full, uint32_t t) __attribute__((always_inline)) {
         constexpr int P = decltype(par)::value;
         constexpr bool HP = decltype(has_prev)::value, FULL = decltype(full)::value;
         char* cur = P == 0 ? ring0 : ring1;
         char* nxt = P == 0 ? ring1 : ring0;
-        char* stage = cur + STAGE + wave * 4096;
+        char* stage = cur + STAGE + wave * 2048;
         tile::wait_vmem<0>();                   // this wave's DMA of tile t (and its last stores)
         tile::ring_barrier();                   // every wave's DMA of t landed; t - 1's reads done
         if (t + 1 < t_hi) issue_a(t + 1, nxt);
-        if constexpr (HP && !FULL) store_edge(acc[1 - P], t - 1);
+        if constexpr (HP && !FULL) store_edge(prev, t - 1);
         // per tap: the LDS byte offset of this lane's A row (its output position's tap pixel, or
         // the zero row) and that row's chunk swizzle
         const uint32_t m = t * BM + 32 * wm + r32;
@@ -419,23 +390,20 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ o
 #pragma unroll
         for (int i = 0; i < PREFETCH; i++) a[i] = rd(i);
 #pragma unroll
+        for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+#pragma unroll
         for (int kb = 0; kb < KB; kb++) {
-            if (kb == 0) {
-                mma_first_a<DT>(acc[P][0], bf[kb][0], a[kb % PREFETCH]);
-                mma_first_v<DT>(acc[P][1], bf[kb][1], a[kb % PREFETCH]);
-            } else {
-                mma_acc_a<DT>(acc[P][0], bf[kb][0], a[kb % PREFETCH]);
-                mma_acc_v<DT>(acc[P][1], bf[kb][1], a[kb % PREFETCH]);
-            }
+            acc = mma<DT>(bf[kb], a[kb % PREFETCH], acc);
             if (kb + PREFETCH < KB) a[kb % PREFETCH] = rd(kb + PREFETCH);
             if constexpr (HP && FULL) {
-                // piece j goes after the MFMAs of K block min(j + 1, KB - 1)
+                // piece j goes after the MFMA of K block min(2 j + 2, KB - 1)
 #pragma unroll
                 for (int j = 0; j < PIECES; j++)
-                    if ((j + 1 < KB ? j + 1 : KB - 1) == kb) store_piece(stage, acc[1 - P], mw, j);
+                    if ((2 * j + 2 < KB ? 2 * j + 2 : KB - 1) == kb) store_piece(stage, prev, mw, j);
             }
         }
-        mfma_drain(acc[P][0], acc[P][1]);
+#pragma unroll
+        for (int w = 0; w < 8; w++) prev[w] = (uint32_t)cvt(acc[2 * w]) | ((uint32_t)cvt(acc[2 * w + 1]) << 16);
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
@@ -446,12 +414,12 @@ __global__ __launch_bounds__(256) void conv_halo_kernel(uint16_t* __restrict__ o
         step(I0{}, BF{}, full, t);
         for (;;) {
             if (++t >= t_hi) {
-                store_all(full, acc[0], t - 1);
+                store_all(full, prev, t - 1);
                 break;
             }
             step(I1{}, BT{}, full, t);
             if (++t >= t_hi) {
-                store_all(full, acc[1], t - 1);
+                store_all(full, prev, t - 1);
                 break;
             }
             step(I0{}, BT{}, full, t);
@@ -964,7 +932,7 @@ int launch_halo(GemmArgs g, const wres::HaloGeom& hg, void* out, const void* xp,
     if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: grid too large");
     auto go = [&](auto kpc) -> int {
         constexpr int KP = decltype(kpc)::value;
-        hipLaunchKernelGGL((wres::conv_halo_kernel<DT, KP>), dim3((uint32_t)blocks), dim3(256), 0, st,
+        hipLaunchKernelGGL((wres::conv_halo_kernel<DT, KP>), dim3((uint32_t)blocks), dim3(512), 0, st,
                            static_cast<uint16_t*>(out), static_cast<const uint16_t*>(xp),
                            static_cast<const uint16_t*>(wp), g, hg, bpc);
         MX_HIP(hipGetLastError());
