@@ -629,6 +629,69 @@ __global__ __launch_bounds__(256) void pack_input_sampled_kernel(S* __restrict__
     *reinterpret_cast<V*>(xp + ((uint64_t)blockIdx.z * OP + q) * Cgp + c0) = v;
 }
 
+// The same sampled pack for a channel-major image (the reference's NCHW tensors seen channels-last:
+// positions contiguous along the last spatial axis, channels far apart), where reading a channel
+// run per lane touches one line per element.  A block takes 64 output positions x 64 channels of
+// one image: lane q of every wave loads sampled position q of its channels -- consecutive lanes,
+// neighbouring samples of one channel row -- into an LDS tile [position][channel dword] (rows of
+// DPR + 1 dwords, so the 64 lanes' writes land in distinct banks); then each thread stores whole
+// 16-byte runs of 4 dwords of a position row.  Channels in [C, Cgp) are written as zeros.
+template <typename S>
+__global__ __launch_bounds__(256) void pack_input_sampled_cm_kernel(S* __restrict__ xp, const S* __restrict__ in,
+                                                                    uint32_t OP, FastDiv osd, int ns, uint32_t C,
+                                                                    uint32_t Cgp, uint64_t sN, uint64_t sC, uint64_t s1,
+                                                                    uint64_t s2, uint32_t st1, uint32_t st2) {
+    constexpr int EPD = 4 / (int)sizeof(S);          // channels per dword
+    constexpr int DPR = 64 / EPD;                     // dwords of a 64-channel position row
+    constexpr int LD = DPR + 1;                       // padded LDS row (dwords)
+    __shared__ uint32_t tile[64 * LD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+    // phase 1: lane = position, dword columns wave, wave + 4, ...
+    {
+        const uint32_t q = min(q0 + (uint32_t)lane, OP - 1);
+        uint64_t off;
+        if (ns == 2) {
+            const uint32_t oh = osd.div(q), ow = q - oh * osd.d;
+            off = (uint64_t)oh * st1 * s1 + (uint64_t)ow * st2 * s2;
+        } else {
+            off = (uint64_t)q * st1 * s1;
+        }
+        const S* src = in + (uint64_t)blockIdx.z * sN + off;
+#pragma unroll
+        for (int i = 0; i < DPR / 4; i++) {
+            const int d = wave + 4 * i;
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < EPD; e++) {
+                const uint32_t c = c0 + (uint32_t)(d * EPD + e);
+                S v = src[(uint64_t)min(c, C - 1) * sC];
+                if (c >= C) v = S(0);
+                uint32_t bitsv = 0;
+                __builtin_memcpy(&bitsv, &v, sizeof(S));
+                word |= bitsv << (8 * sizeof(S) * e);
+            }
+            tile[lane * LD + d] = word;
+        }
+    }
+    __syncthreads();
+    // phase 2: 16-byte chunk k (dwords 4 k .. 4 k + 3) of position row r
+    constexpr int CPR = DPR / 4;                      // chunks per position row
+#pragma unroll
+    for (int i = 0; i < 64 * CPR / 256; i++) {
+        const int idx = (int)threadIdx.x + 256 * i;
+        const int r = idx / CPR, k = idx % CPR;
+        const uint32_t q = q0 + (uint32_t)r, c = c0 + (uint32_t)(4 * k * EPD);
+        if (q >= OP || c >= Cgp) continue;
+        uint4 v;
+        v.x = tile[r * LD + 4 * k];
+        v.y = tile[r * LD + 4 * k + 1];
+        v.z = tile[r * LD + 4 * k + 2];
+        v.w = tile[r * LD + 4 * k + 3];
+        *reinterpret_cast<uint4*>(xp + ((uint64_t)blockIdx.z * OP + q) * Cgp + c) = v;
+    }
+}
+
 // ------------------------------------------------------------------ direct kernel
 struct DirectDesc {
     int ns;
@@ -1056,10 +1119,20 @@ int launch_mfma_path(const ConvShape& cs, const Plan& p, const int* pad_lo, cons
         constexpr uint32_t VE = 16 / sizeof(S);
         uint32_t OP = 1;
         for (int d = 0; d < cs.ns; d++) OP *= cs.OS[d];
-        const dim3 grid((OP + 31) / 32, (p.Cgp + 8 * VE - 1) / (8 * VE), cs.N);
-        hipLaunchKernelGGL((pack_input_sampled_kernel<S>), grid, dim3(256), 0, st, xs, static_cast<const S*>(in), OP,
-                           FastDiv(cs.OS[cs.ns - 1]), cs.ns, cs.C, p.Cgp, cs.in_s[0], cs.in_s[cs.ns + 1], cs.in_s[1],
-                           cs.ns == 2 ? cs.in_s[2] : 0, (uint32_t)stride[0], cs.ns == 2 ? (uint32_t)stride[1] : 0u);
+        if (cs.in_s[cs.ns] == 1 && cs.in_s[cs.ns + 1] != 1) {
+            // channel-major image (NCHW seen channels-last): load along the spatial axis
+            const dim3 grid((OP + 63) / 64, (p.Cgp + 63) / 64, cs.N);
+            hipLaunchKernelGGL((pack_input_sampled_cm_kernel<S>), grid, dim3(256), 0, st, xs, static_cast<const S*>(in),
+                               OP, FastDiv(cs.OS[cs.ns - 1]), cs.ns, cs.C, p.Cgp, cs.in_s[0], cs.in_s[cs.ns + 1],
+                               cs.in_s[1], cs.ns == 2 ? cs.in_s[2] : 0, (uint32_t)stride[0],
+                               cs.ns == 2 ? (uint32_t)stride[1] : 0u);
+        } else {
+            const dim3 grid((OP + 31) / 32, (p.Cgp + 8 * VE - 1) / (8 * VE), cs.N);
+            hipLaunchKernelGGL((pack_input_sampled_kernel<S>), grid, dim3(256), 0, st, xs, static_cast<const S*>(in),
+                               OP, FastDiv(cs.OS[cs.ns - 1]), cs.ns, cs.C, p.Cgp, cs.in_s[0], cs.in_s[cs.ns + 1],
+                               cs.in_s[1], cs.ns == 2 ? cs.in_s[2] : 0, (uint32_t)stride[0],
+                               cs.ns == 2 ? (uint32_t)stride[1] : 0u);
+        }
         MX_HIP(hipGetLastError());
         const void* wq = kern;
         if (p.pack_k || flip) {

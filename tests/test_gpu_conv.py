@@ -124,6 +124,7 @@ def test_conv2d_mfma(mx, orc, dt, case):
     (2, 40, 9, 9, 16, 2, 2, "nhwc"),       # channels-last input with padded channels (40 -> 64 / 64 / 64)
     (2, 48, 10, 12, 40, 2, 1, "nchw"),     # stride 2 along H only
     (1, 16, 7, 16, 8, 1, 4, "nhwc"),       # stride 4 along W only
+    (2, 130, 30, 29, 24, 2, 2, "nchw"),    # channel-major pack: 4 x 3 position / channel blocks, ragged
 ])
 def test_conv2d_1x1_strided_sampled_pack(mx, orc, dt, case):
     code = getattr(mx, dt)
