@@ -822,6 +822,8 @@ def main():
                    "executor": f"compiled graph, execute + wait per step, {g['streams']} streams"},
         "roofline": {"bound": "hbm", "achieved": round(r["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["achieved"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(r["dominant"]),
+                     "traffic_source": "profiles/traffic.json: rocprofv3 FETCH_SIZE x 1.9996 + WRITE_SIZE for this "
+                                       "kernel (counter passes run apart from the bench, not in this run)",
                      "kernel": r["dominant"], "members": r["dominant_members"],
                      "bytes_per_launch": r["dominant_bytes"], "avg_ms": round(r["dominant_ms"], 5)},
         "cpu_baseline": cpu,
