@@ -176,13 +176,16 @@ static_assert(MAX_KP * WSLOT <= 2 * RING + WSLOT, "kernel row staging");
 static_assert(2 * RING + WSLOT <= 160 * 1024, "LDS of a workgroup");
 constexpr int PREFETCH = 4;                     // A fragments in flight ahead of the MFMAs
 
+// An LDS row is one 128-byte K pair: pixel q of a halo owns rows q cp .. q cp + cp - 1 (cp = K pairs
+// per pixel, Cgp / 64), and K pair p of the kernel is channel block p % cp of kernel position p / cp.
 struct HaloGeom {
     FastDiv s0, s1;                 // spatial extents (1-D: s0 = 1)
-    int32_t rlo;                    // halo rows before a tile's first position
+    FastDiv cp;                     // K pairs per pixel
+    int32_t rlo;                    // halo pixels before a tile's first position
     uint32_t hrows;                 // halo rows DMA'd per tile (a multiple of 8, <= MAX_HALO)
-    uint32_t npix;                  // input pixel rows (batch x spatial)
-    int32_t sh[MAX_KP];             // per kernel position: pixel shift
-    int32_t dk0[MAX_KP], dk1[MAX_KP];   // per kernel position: offset along each axis
+    uint32_t npix;                  // input pixels (batch x spatial)
+    int32_t sh[MAX_KP];             // per K pair: row shift (pixel shift x cp + channel block)
+    int32_t dk0[MAX_KP], dk1[MAX_KP];   // per K pair: its kernel position's offset along each axis
     uint32_t on, os0, os1;          // output element strides: batch, axis 0, axis 1
 };
 
@@ -223,13 +226,14 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ o
         uint32_t M, N, K, tiles_m;
     } g = {ga.M, ga.N, ga.K, ga.tiles_m};
     struct {
-        FastDiv s0, s1;
+        FastDiv s0, s1, cp;
         int32_t rlo;
         uint32_t hrows, npix, on, os0, os1;
         int32_t sh[KP], dk0[KP], dk1[KP];
     } hg;
     hg.s0 = hga.s0;
     hg.s1 = hga.s1;
+    hg.cp = hga.cp;
     hg.rlo = hga.rlo;
     hg.hrows = hga.hrows;
     hg.npix = hga.npix;
@@ -271,19 +275,22 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ o
 
 #if __HIP_DEVICE_COMPILE__                               // (the buffer resource type is device-only)
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<S*>(xp), 0, (int)(hg.npix * (uint32_t)tile::ROWB), 0x00020000);
+        const_cast<S*>(xp), 0, (int)(hg.npix * hg.cp.d * (uint32_t)tile::ROWB), 0x00020000);
 #endif
-    // the halo of tile t: rows r = 0 .. hrows - 1 are input pixels m0 - rlo + r (clamped into the
-    // image: a clamped row is read only by taps off the image, which take the zero row); DMA
-    // instruction i fills rows 8 i .. 8 i + 7, lane L row 8 i + L / 8, stored chunk L % 8
+    // the halo of tile t: row r = 0 .. hrows - 1 is channel block r % cp of input pixel
+    // m0 - rlo + r / cp (clamped into the image: a clamped pixel is read only by taps off the image,
+    // which take the zero row); DMA instruction i fills rows 8 i .. 8 i + 7, lane L row 8 i + L / 8,
+    // stored chunk L % 8
     auto issue_a = [&](uint32_t t, char* buf) __attribute__((always_inline)) {
         const int32_t first = (int32_t)(t * BM) - hg.rlo;
         const int nd = (int)(hg.hrows / 8);
         for (int i = wave; i < nd; i += NW) {
-            const int r = 8 * i + lane / 8;
-            int32_t pix = first + r;
+            const uint32_t r = (uint32_t)(8 * i + lane / 8);
+            const uint32_t rq = hg.cp.div(r), blk = r - rq * hg.cp.d;
+            int32_t pix = first + (int32_t)rq;
             pix = pix < 0 ? 0 : (pix >= (int32_t)hg.npix ? (int32_t)hg.npix - 1 : pix);
-            const uint32_t off = (uint32_t)pix * (uint32_t)tile::ROWB + (uint32_t)tile::swz(r, lane % 8) * 16u;
+            const uint32_t off = ((uint32_t)pix * hg.cp.d + blk) * (uint32_t)tile::ROWB +
+                                 (uint32_t)tile::swz((int)r, lane % 8) * 16u;
 #if __HIP_DEVICE_COMPILE__
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(buf + i * 1024),
                                                      16, off, 0, 0, 0);
@@ -372,7 +379,7 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ o
         const uint32_t m = t * BM + 32 * wm + r32;
         const uint32_t q1 = hg.s1.div(m), o1 = m - q1 * hg.s1.d;
         const uint32_t o0 = q1 - hg.s0.div(q1) * hg.s0.d;
-        const int base = 32 * wm + r32 + hg.rlo;
+        const int base = (32 * wm + r32 + hg.rlo) * (int)hg.cp.d;
         int roff[KP], rsw[KP];
 #pragma unroll
         for (int p = 0; p < KP; p++) {
@@ -940,18 +947,22 @@ bool halo_enabled() {
 }
 
 // The halo geometry of a same convolution, or false when the halo kernel does not apply: one
-// group, 64 channels per K pair (16-bit), at most 9 kernel positions, stride 1 and each output
-// extent equal to its input extent, the halo within a ring half, C rows in whole 16-byte units.
+// group, 2 or more kernel positions and at most 9 K pairs of 64 channels (16-bit) over all of
+// them, stride 1 and each output extent equal to its input extent, the halo within a ring half, C
+// rows in whole 16-byte units.
 template <int NS>
 bool halo_geom(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, const int* stride, const int* dil,
                wres::HaloGeom& hg) {
-    if (cs.groups != 1 || Cgp * 2 != (uint32_t)tile::ROWB || cs.out_s[NS + 1] != 1) return false;
+    if (cs.groups != 1 || (Cgp * 2) % (uint32_t)tile::ROWB || cs.out_s[NS + 1] != 1) return false;
+    const uint32_t cp = Cgp * 2 / (uint32_t)tile::ROWB;
     uint32_t kpos = 1;
     for (int d = 0; d < NS; d++) {
         if (stride[d] != 1 || cs.OS[d] != cs.S[d]) return false;
         kpos *= cs.K[d];
     }
-    if (kpos > (uint32_t)wres::MAX_KP) return false;
+    // a 1 x 1 kernel reads each pixel once, so a halo saves nothing: the tile kernel's GEMM runs it
+    // faster (config 4's 1 x 1 stride-2 product after its pack: 7.0 against 7.8 us)
+    if (kpos < 2 || kpos * cp > (uint32_t)wres::MAX_KP) return false;
     for (int a = 0; a <= NS; a++)
         if ((cs.out_s[a] * 2) % 16) return false;
     hg = wres::HaloGeom{};
@@ -967,14 +978,22 @@ bool halo_geom(const ConvShape& cs, uint32_t Cgp, const int* pad_lo, const int* 
             const int64_t sh = a0 * S1 + a1;
             if (sh < lo) lo = sh;
             if (sh > hi) hi = sh;
-            hg.dk0[t] = (int32_t)a0;
-            hg.dk1[t] = (int32_t)a1;
-            hg.sh[t] = (int32_t)sh;
+            for (uint32_t b = 0; b < cp; b++) {
+                hg.dk0[t * cp + b] = (int32_t)a0;
+                hg.dk1[t * cp + b] = (int32_t)a1;
+                hg.sh[t * cp + b] = (int32_t)(sh * cp + b);
+            }
         }
-    const int64_t rows = (wres::BM + (-lo) + hi + 7) / 8 * 8;
+    const int64_t rows = ((wres::BM + (-lo) + hi) * (int64_t)cp + 7) / 8 * 8;
     if (rows > wres::MAX_HALO) return false;
+    // the halo must save DMA against gathering each K pair's 64 rows: at 352 halo rows for 384
+    // gathered (3 x 1 over 128 channels of 56-pixel rows) the tile kernel ran 18.2 against 19.7 us;
+    // at 136 / 384 (1 x 3), 360 / 576 (3 x 1, 192 channels) and 184 / 576 (config 4) the halo kernel
+    // ran 17.5 / 14.1 / 21.5 against 18.2 / 18.9 / 23.8 us
+    if (4 * rows > 3 * (int64_t)wres::BM * kpos * cp) return false;
     hg.s0 = FastDiv(S0);
     hg.s1 = FastDiv(S1);
+    hg.cp = FastDiv(cp);
     hg.rlo = (int32_t)(-lo);
     hg.hrows = (uint32_t)rows;
     hg.npix = (uint32_t)((uint64_t)cs.N * S0 * S1);

@@ -222,7 +222,7 @@ def test_conv2d_many_tiles(mx, orc, dt, case):
     (4, 30, 70, 64, 128, 3, 3, 1, 1),      # 8400 positions: 132 tiles, the last one 16 rows
     (5, 64, 64, 64, 128, 1, 3, 1, 1),      # 320 tiles: blocks walk two tiles through the ring
     (1, 20, 21, 48, 256, 3, 3, 2, 2),      # dilation 2, two full column groups, 48 -> 64 channels
-    (1, 6, 200, 64, 128, 3, 3, 1, 1),      # 200-pixel rows: a 472-row halo per tile
+    (1, 6, 150, 64, 128, 3, 3, 1, 1),      # 150-pixel rows: a 368-row halo per tile
     (2, 13, 17, 64, 200, 3, 3, 1, 1),      # a full column group and a 72-channel one
 ])
 def test_conv2d_same_halo(mx, orc, dt, case):

@@ -24,6 +24,8 @@ CASES = [
     (4, 56, 56, 64, 128, 3, 3, 1, 1, "FLOAT16"),    # config 4's 3x3 case at batch 4: 196 tiles
     (3, 20, 33, 40, 200, 3, 3, 2, 2, "BFLOAT16"),   # dilation, padded channels, a 72-channel group
     (2, 31, 17, 64, 128, 1, 3, 1, 1, "FLOAT16"),    # a 1 x 3 kernel, a 16-row tail tile
+    (2, 20, 22, 128, 192, 1, 3, 1, 1, "FLOAT16"),   # 128 channels: 2 K pairs per pixel, 6 in all
+    (3, 9, 13, 130, 128, 3, 1, 1, 1, "BFLOAT16"),   # 130 channels padded to 192: 3 K pairs per pixel, 9 in all
 ]
 
 # run in this process and, with the tile kernel forced, in a child process
