@@ -207,7 +207,8 @@ __device__ __forceinline__ tile::f16v mma(const typename FragT<DT>::V& b, const 
 // wave per SIMD holding 64 channels (two MFMAs per A fragment read) kept the matrix cores busy
 // only about half the time: a lone wave's MFMAs issue one after another with gaps that a second
 // wave fills.
-template <int DT, int KP>
+// CP1: one K pair per pixel (cp = 1, 64 channels), with the pair arithmetic folded away.
+template <int DT, int KP, bool CP1>
 __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ out, const uint16_t* __restrict__ xp,
                                                         const uint16_t* __restrict__ wp, GemmArgs ga, HaloGeom hga,
                                                         uint32_t bpc) {
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ o
 
 #if __HIP_DEVICE_COMPILE__                               // (the buffer resource type is device-only)
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<S*>(xp), 0, (int)(hg.npix * hg.cp.d * (uint32_t)tile::ROWB), 0x00020000);
+        const_cast<S*>(xp), 0, (int)(hg.npix * (CP1 ? 1u : hg.cp.d) * (uint32_t)tile::ROWB), 0x00020000);
 #endif
     // the halo of tile t: row r = 0 .. hrows - 1 is channel block r % cp of input pixel
     // m0 - rlo + r / cp (clamped into the image: a clamped pixel is read only by taps off the image,
@@ -286,10 +287,10 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ o
         const int nd = (int)(hg.hrows / 8);
         for (int i = wave; i < nd; i += NW) {
             const uint32_t r = (uint32_t)(8 * i + lane / 8);
-            const uint32_t rq = hg.cp.div(r), blk = r - rq * hg.cp.d;
+            const uint32_t rq = CP1 ? r : hg.cp.div(r), blk = CP1 ? 0u : r - rq * hg.cp.d;
             int32_t pix = first + (int32_t)rq;
             pix = pix < 0 ? 0 : (pix >= (int32_t)hg.npix ? (int32_t)hg.npix - 1 : pix);
-            const uint32_t off = ((uint32_t)pix * hg.cp.d + blk) * (uint32_t)tile::ROWB +
+            const uint32_t off = ((uint32_t)pix * (CP1 ? 1u : hg.cp.d) + blk) * (uint32_t)tile::ROWB +
                                  (uint32_t)tile::swz((int)r, lane % 8) * 16u;
 #if __HIP_DEVICE_COMPILE__
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(buf + i * 1024),
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(uint16_t* __restrict__ o
         const uint32_t m = t * BM + 32 * wm + r32;
         const uint32_t q1 = hg.s1.div(m), o1 = m - q1 * hg.s1.d;
         const uint32_t o0 = q1 - hg.s0.div(q1) * hg.s0.d;
-        const int base = (32 * wm + r32 + hg.rlo) * (int)hg.cp.d;
+        const int base = (32 * wm + r32 + hg.rlo) * (CP1 ? 1 : (int)hg.cp.d);
         int roff[KP], rsw[KP];
 #pragma unroll
         for (int p = 0; p < KP; p++) {
@@ -1014,9 +1015,14 @@ int launch_halo(GemmArgs g, const wres::HaloGeom& hg, void* out, const void* xp,
     if (blocks > 0x7fffffffull) return fail(MX_ERR_INVALID_ARG, "mx_launch_conv_nd: grid too large");
     auto go = [&](auto kpc) -> int {
         constexpr int KP = decltype(kpc)::value;
-        hipLaunchKernelGGL((wres::conv_halo_kernel<DT, KP>), dim3((uint32_t)blocks), dim3(512), 0, st,
-                           static_cast<uint16_t*>(out), static_cast<const uint16_t*>(xp),
-                           static_cast<const uint16_t*>(wp), g, hg, bpc);
+        if (hg.cp.d == 1)
+            hipLaunchKernelGGL((wres::conv_halo_kernel<DT, KP, true>), dim3((uint32_t)blocks), dim3(512), 0, st,
+                               static_cast<uint16_t*>(out), static_cast<const uint16_t*>(xp),
+                               static_cast<const uint16_t*>(wp), g, hg, bpc);
+        else
+            hipLaunchKernelGGL((wres::conv_halo_kernel<DT, KP, false>), dim3((uint32_t)blocks), dim3(512), 0, st,
+                               static_cast<uint16_t*>(out), static_cast<const uint16_t*>(xp),
+                               static_cast<const uint16_t*>(wp), g, hg, bpc);
         MX_HIP(hipGetLastError());
         return MX_OK;
     };
