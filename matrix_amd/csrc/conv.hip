@@ -139,19 +139,21 @@ struct ConvSrc {
 
 // ------------------------------------------------------------------ weight-resident halo kernel
 // A "same" convolution (stride 1, each output extent equal to its input extent, 1 or 2 spatial
-// axes) of a 16-bit type, one group, channels padded to exactly one K pair (Cgp x 2 bytes = 128:
-// 64 channels), at most 9 kernel positions.  Output position m (flattened over batch and spatial
-// axes) then reads, at kernel position t, input pixel m + sh_t (sh_t = sum_d (k_d dil_d - pad_d)
-// x the pixel stride of axis d) whenever that tap lies inside the image, zeros otherwise.
+// axes) of a 16-bit type, one group, two or more kernel positions and at most 9 K pairs (64
+// channels each, Cgp / 64 per kernel position) over all of them, whose halo saves reads (see
+// halo_geom).  Output position m (flattened over batch and spatial axes) then reads, at kernel
+// position t, input pixel m + sh_t (sh_t = sum_d (k_d dil_d - pad_d) x the pixel stride of axis d)
+// whenever that tap lies inside the image, zeros otherwise.
 //
 // * The kernel stays in registers.  A workgroup of 8 waves (two per SIMD) owns a column group of
 //   128 output channels; wave (wm, wn) holds the MFMA B fragments of channels 32 wn .. 32 wn + 31
 //   over all of K for the workgroup's whole life (KP x 16 registers), loaded once through LDS.
-// * A tile is 64 consecutive output positions.  Its A operand for all KP taps is one halo: the
-//   input pixel rows m0 - rlo .. m0 + 63 + rhi, 128 bytes each, DMA'd once into one half of a
-//   two-tile LDS ring (178 rows for a 3 x 3 kernel over 56-pixel image rows, a third of the bytes
-//   of gathering every tap's 64 rows).  A fragment of tap t reads LDS row (m - m0) + rlo + sh_t,
-//   or a zero row for a tap off the image.  The next tile's halo lands while this one runs.
+// * A tile is 64 consecutive output positions.  Its A operand for all KP K pairs is one halo: the
+//   input pixels m0 - rlo .. m0 + 63 + rhi, Cgp x 2 bytes each, DMA'd once into one half of a
+//   two-tile LDS ring (178 rows of 128 bytes for a 3 x 3 kernel over 64 channels of 56-pixel image
+//   rows, a third of the bytes of gathering every tap's 64 rows).  A fragment of tap t reads the
+//   LDS rows of pixel (m - m0) + rlo + sh_t, or a zero row for a tap off the image.  The next
+//   tile's halo lands while this one runs.
 // * Wave (wm, wn) computes output rows 32 wm .. + 31 x its 32 channels: per K block of 16, one
 //   1 KB A fragment read from LDS for one MFMA.
 // * The previous tile's results, rounded to 16 bits, are stored in pieces between the current
